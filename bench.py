@@ -1,0 +1,322 @@
+#!/usr/bin/env python3
+"""Benchmark of the minicompiler HIP backend on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mlp|gelu|batchnorm|gemm_fp32|gemm_bf16]
+
+A step is one enqueue of the compiled graph (every kernel of one forward
+pass over one batch of synthetic, seeded input already resident in HBM).
+The headline workload is BASELINE config 2, the fp32 MLP block
+(mlp_gelu.mcg) at B=8192: GEMM, fused bias+GELU, GEMM, fused
+bias+residual. W untimed steps, then exactly K timed steps between two HIP
+events on the executable's stream, with a HIP event before every launch so
+each kernel's duration comes from the same timed region.
+
+Prints ONE JSON line. `value` is the step's GEMM throughput (TFLOP/s = the
+two GEMMs' 2MNK FLOPs per step / ms_per_step). `roofline` is for the
+kernel that takes the most time; `kernels` lists every launch with its
+algorithmic work, achieved rate and fraction of the MI355X peak (HBM 8 TB/s;
+FP32 matrix 157.3 TFLOP/s; dense bf16/fp16 2.5 PFLOP/s). `configs` adds the
+other BASELINE configs measured in the same process (skip with --quick).
+`cpu_baseline` times the CPU oracle (a C++ restatement of the reference's
+Eigen backend, test infrastructure) on a bounded row sample of the same
+workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_BF16_TFLOPS = 2500.0
+METRIC = "fused-kernel HBM GB/s + GEMM TFLOPS, % of MI355X roofline, 1 GPU"
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def node_work(graph: dict) -> list[dict]:
+    """Algorithmic work of each launch (compute nodes in id order): 2MNK FLOPs
+    for a matmul; for an elementwise kernel the bytes of its output plus each
+    distinct non-scalar operand read once (the reference's bytes_moved,
+    bench/bench_cuda.cpp:79-95)."""
+    nodes = graph["nodes"]
+    out = []
+    for n in nodes:
+        if n["op_name"] in ("input", "const"):
+            continue
+        if n["op_name"] == "matmul":
+            (m, k), (_, nn) = nodes[n["inputs"][0]]["shape"], nodes[n["inputs"][1]]["shape"]
+            out.append({"kind": "gemm", "flop": 2.0 * m * nn * k, "m": m, "n": nn, "k": k})
+        else:
+            size = lambda s: int(np.prod(s, dtype=np.int64)) if s else 1
+            b = 4 * size(n["shape"])
+            for i in sorted(set(n["inputs"])):
+                sz = size(nodes[i]["shape"])
+                if sz > 1:
+                    b += 4 * sz
+            out.append({"kind": "elementwise", "bytes": float(b)})
+    return out
+
+
+def rate_entry(name: str, work: dict, ms: float, gemm_peak: float = PEAK_FP32_TFLOPS) -> dict:
+    if work["kind"] == "gemm":
+        tflops = work["flop"] / (ms * 1e-3) / 1e12
+        return {"launch": name, "ms": ms, "flop": work["flop"], "tflops": tflops, "bound": "mfma",
+                "peak": gemm_peak, "frac": tflops / gemm_peak}
+    gbs = work["bytes"] / (ms * 1e-3) / 1e9
+    return {"launch": name, "ms": ms, "bytes": work["bytes"], "gbs": gbs, "bound": "hbm", "peak": PEAK_HBM_GBS,
+            "frac": gbs / PEAK_HBM_GBS}
+
+
+def time_graph(mc, compiled, steps: int, warmup: int, rotations=None) -> dict:
+    """W warmup steps, then K steps timed between HIP events with per-launch
+    events. `rotations`: list of (input_ptrs, output_ptrs) bound in turn, so
+    consecutive steps touch different buffers (defeats the 256 MB MALL)."""
+    def bind(i):
+        if rotations:
+            ins, outs = rotations[i % len(rotations)]
+            compiled.bind_inputs(ins)
+            compiled.bind_outputs(outs)
+
+    stream = compiled.stream
+    for i in range(warmup):
+        bind(i)
+        compiled.enqueue()
+    compiled.synchronize()
+    compiled.profile_start(steps)
+    start, stop = mc.Event(), mc.Event()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        bind(i)
+        compiled.enqueue_profiled()
+    stop.record(stream)
+    compiled.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_ms(stop)
+    per_launch = compiled.profile_read()  # [steps, launches]
+    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall,
+            "launch_ms": per_launch.mean(axis=0).tolist(), "launch_ms_min": per_launch.min(axis=0).tolist()}
+
+
+def bench_mlp(mc, batch: int, steps: int, warmup: int) -> dict:
+    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch})
+    x = mc.uniform(batch * 512, 1, -1.0, 1.0)
+    c.upload([x])
+    t = time_graph(mc, c, steps, warmup)
+    work = node_work(c.graph())
+    names = c.launch_names
+    kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
+    flop = sum(w["flop"] for w in work if w["kind"] == "gemm")
+    return {"compiled": c, "timing": t, "kernels": kernels, "gemm_flop": flop,
+            "value": flop / (t["ms_per_step"] * 1e-3) / 1e12, "jit_ms": c.jit_compile_ms}
+
+
+def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, warmup: int) -> dict:
+    """One fused group, rotating over input/output buffer sets whose total
+    footprint exceeds twice the MALL."""
+    c = mc.Compiled(path=mc.graph_path(name), dims=dims)
+    n_in, n_out = c.input_sizes[0], c.output_sizes[0]
+    set_bytes = 4 * (n_in + n_out)
+    sets = max(2, -(-2 * MALL_BYTES // set_bytes) + 1)
+    x = make_input(n_in)
+    bufs = []
+    for _ in range(sets):
+        bi, bo = mc.DeviceBuffer.from_array(x), mc.DeviceBuffer(4 * n_out)
+        bufs.append((bi, bo))
+    rot = [([bi.ptr], [bo.ptr]) for bi, bo in bufs]
+    t = time_graph(mc, c, steps, warmup, rot)
+    work = node_work(c.graph())
+    (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
+    return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
+            "gbs": k["gbs"], "frac": k["frac"], "launch_ms_min": t["launch_ms_min"][0]}
+
+
+def time_gemm(mc, launch, steps: int, warmup: int) -> float:
+    s = mc.Stream()
+    for _ in range(warmup):
+        launch(s)
+    evs = [mc.Event() for _ in range(steps + 1)]
+    evs[0].record(s)
+    for i in range(steps):
+        launch(s)
+        evs[i + 1].record(s)
+    s.synchronize()
+    return float(np.median([evs[i].elapsed_ms(evs[i + 1]) for i in range(steps)]))
+
+
+def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]:
+    out = []
+    for m, n, k in shapes:
+        kernel = mc.resolve_matmul_kernel("auto", m, n, k, cus)
+        splits = mc.matmul_splits(kernel, m, n, k, cus)
+        a = mc.DeviceBuffer.from_array(mc.uniform(m * k, 1, -1.0, 1.0))
+        b = mc.DeviceBuffer.from_array(mc.uniform(k * n, 2, -1.0, 1.0))
+        c = mc.DeviceBuffer(4 * m * n)
+        ws_bytes = mc.matmul_workspace_bytes(kernel, m, n, splits)
+        ws = mc.DeviceBuffer(ws_bytes) if ws_bytes else None
+        ms = time_gemm(mc, lambda s: mc.launch_matmul(kernel, a.ptr, b.ptr, c.ptr, m, n, k, s, splits,
+                                                       ws.ptr if ws else None), steps, warmup)
+        flop = 2.0 * m * n * k
+        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "ms": ms,
+             "tflops": flop / (ms * 1e-3) / 1e12}
+        e["frac"] = e["tflops"] / PEAK_FP32_TFLOPS
+        if m == 16:  # HBM-bound skinny shape: report bytes too
+            byt = 4.0 * (m * k + k * n + m * n)
+            e["gbs"] = byt / (ms * 1e-3) / 1e9
+            e["frac_hbm"] = e["gbs"] / PEAK_HBM_GBS
+        out.append(e)
+        log(f"gemm fp32 {m}x{n}x{k} {kernel}: {ms:.3f} ms {e['tflops']:.1f} TFLOP/s")
+    return out
+
+
+def bench_gemm_lowp(mc, shapes, steps: int, warmup: int) -> list[dict]:
+    out = []
+    for m, n, k in shapes:
+        a32 = mc.DeviceBuffer.from_array(mc.uniform(m * k, 1, -1.0, 1.0))
+        b32 = mc.DeviceBuffer.from_array(mc.uniform(k * n, 2, -1.0, 1.0))
+        for kernel, dtype in (("tensor_core_bf16", mc.DTYPE_BF16), ("tensor_core_f16", mc.DTYPE_F16)):
+            a, b = mc.DeviceBuffer(2 * m * k), mc.DeviceBuffer(2 * k * n)
+            mc.convert_f32(dtype, a32.ptr, a.ptr, m * k)
+            mc.convert_f32(dtype, b32.ptr, b.ptr, k * n)
+            c = mc.DeviceBuffer(4 * m * n)
+            ms = time_gemm(mc, lambda s: mc.launch_matmul_lowp(kernel, dtype, a.ptr, b.ptr, c.ptr, m, n, k, s),
+                           steps, warmup)
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            out.append({"m": m, "n": n, "k": k, "kernel": kernel, "inputs": "bf16" if dtype == 1 else "fp16",
+                        "ms": ms, "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
+            log(f"gemm {kernel} {m}x{n}x{k}: {ms:.3f} ms {tf:.1f} TFLOP/s")
+            del a, b, c
+    return out
+
+
+def cpu_baseline(batch_rows: int, seconds: float) -> dict:
+    """The CPU oracle (restating the reference's Eigen backend) on the first
+    `batch_rows` rows of the MLP workload, one thread, repeated for about
+    `seconds`. Throughput in the headline unit."""
+    import minicompiler_amd as mc
+    from oracle import oracle as orc
+
+    orc.set_threads(1)
+    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch_rows}, backend="none")
+    g = c.graph()
+    consts = {n["id"]: c.constant(n["id"]) for n in g["nodes"] if n["op_name"] == "const"}
+    x = mc.uniform(batch_rows * 512, 1, -1.0, 1.0)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.evaluate(g, consts, [x])
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= 2:
+            break
+    per = el / reps
+    flop = 4.0 * batch_rows * 512 * 2048
+    return {"value": flop / per / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"mlp_gelu rows 0..{batch_rows - 1} of the B=8192 batch, {reps} reps, {per * 1e3:.1f} ms/rep, "
+                      f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM), 1 thread, {os.cpu_count()} host cores"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="mlp", choices=["mlp", "gelu", "batchnorm", "gemm_fp32", "gemm_bf16"])
+    ap.add_argument("--batch", type=int, default=8192)
+    ap.add_argument("--quick", action="store_true", help="headline workload only (no other configs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the multi-GPU sharding is a design only "
+              "(see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import minicompiler_amd as mc
+
+    dev = mc.device_json()
+    cus = dev["cu_count"]
+    log(f"device: {dev['name']} {dev['arch']} CUs={cus} clock={dev['clock_mhz']} MHz")
+    line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded splitmix64 uniform/normal, "
+                                                            "random-init constants of the graph)"}
+
+    if args.workload == "mlp":
+        r = bench_mlp(mc, args.batch, args.steps, args.warmup)
+        ks = r["kernels"]
+        dom = max(ks, key=lambda e: e["ms"])
+        line.update({"value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["timing"]["ms_per_step"],
+                     "dtype": "f32",
+                     "config": {"workload": f"mlp_gelu B={args.batch} D=512 H=2048 fp32 (BASELINE config 2)",
+                                "global_batch": args.batch, "matmul": ",".join(r["compiled"].matmul_kernels)}})
+        unit = "TFLOP/s" if dom["bound"] == "mfma" else "GB/s"
+        achieved = dom["tflops"] if dom["bound"] == "mfma" else dom["gbs"]
+        line["roofline"] = {"bound": dom["bound"], "kernel": dom["launch"], "achieved": achieved,
+                            "peak": dom["peak"], "unit": unit, "frac": dom["frac"], "traffic": None}
+        line["kernels"] = ks
+        fused = [k for k in ks if k["bound"] == "hbm"]
+        line["fused_gbs"] = sum(k["bytes"] for k in fused) / (sum(k["ms"] for k in fused) * 1e-3) / 1e9 if fused else None
+        line["jit_compile_ms"] = r["jit_ms"]
+    else:
+        line["unit"] = "GB/s" if args.workload in ("gelu", "batchnorm") else "TFLOP/s"
+
+    if args.workload in ("gelu", "batchnorm") or (args.workload == "mlp" and not args.quick):
+        cfgs = line.setdefault("configs", {})
+        if args.workload != "batchnorm":
+            cfgs["gelu_4096x4096"] = bench_elementwise_graph(
+                mc, "gelu_chain", {"M": 4096, "N": 4096}, lambda n: mc.uniform(n, 1, -3.0, 3.0), args.steps, args.warmup)
+            log(f"gelu: {cfgs['gelu_4096x4096']['gbs']:.0f} GB/s")
+        if args.workload != "gelu":
+            cfgs["batchnorm_relu_200704x256"] = bench_elementwise_graph(
+                mc, "batchnorm_relu", {"R": 200704, "C": 256}, lambda n: mc.normal(n, 1, 0.0, 1.0), args.steps,
+                args.warmup)
+            log(f"batchnorm: {cfgs['batchnorm_relu_200704x256']['gbs']:.0f} GB/s")
+        if args.workload in ("gelu", "batchnorm"):
+            k = next(iter(cfgs.values()))
+            line.update({"value": k["gbs"], "ms_per_step": k["ms_per_step"], "dtype": "f32",
+                         "config": {"workload": k["config"], **k["dims"]},
+                         "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
+                                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
+    if args.workload == "gemm_fp32" or (args.workload == "mlp" and not args.quick):
+        shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384), (16, 4096, 4096)]
+        g = bench_gemm_fp32(mc, cus, shapes, 10, 3)
+        line.setdefault("configs", {})["gemm_fp32"] = g
+        if args.workload == "gemm_fp32":
+            top = g[2]
+            line.update({"value": top["tflops"], "ms_per_step": top["ms"], "dtype": "f32",
+                         "config": {"workload": "fp32 gemm 8192^3 (BASELINE config 4)"},
+                         "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
+                                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
+    if args.workload == "gemm_bf16" or (args.workload == "mlp" and not args.quick):
+        g = bench_gemm_lowp(mc, [(8192, 8192, 8192), (4096, 14336, 4096)], 10, 3)
+        line.setdefault("configs", {})["gemm_bf16_fp16"] = g
+        if args.workload == "gemm_bf16":
+            top = g[0]
+            line.update({"value": top["tflops"], "ms_per_step": top["ms"], "dtype": "bf16",
+                         "config": {"workload": "bf16 gemm 8192^3, bf16 inputs in HBM (BASELINE config 5)"},
+                         "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
+                                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
+
+    line["device"] = {k: dev[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
+    if not args.no_cpu_baseline and args.workload == "mlp":
+        line["cpu_baseline"] = cpu_baseline(256, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

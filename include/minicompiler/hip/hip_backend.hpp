@@ -1,0 +1,133 @@
+#pragma once
+
+// The HIP backend for AMD Instinct MI355X (gfx950 / CDNA4). It takes the
+// place of the reference's CUDA backend behind the same Backend/Executable
+// interface (reference: include/minicompiler/cuda/cuda_backend.hpp:20-107).
+// This header includes no HIP header: every HIP call goes through the
+// library's thin C-ABI layer.
+
+#include "minicompiler/graph.hpp"
+#include "minicompiler/result.hpp"
+#include "minicompiler/runtime/backend.hpp"
+
+#include <cstddef>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace minicompiler::hip {
+
+// The matmul kernels, same names as the reference's MatmulKernel
+// (cuda_backend.hpp:20-37). On CDNA4:
+//   Naive, Tiled, RegisterTiled128, RegisterTiled64: FP32 on the vector ALU
+//     (one output per lane; 32x32 LDS tiles; 128x128 and 64x64 tiles with an
+//     8x8 / 4x4 register block per lane).
+//   Vectorized: 128x128 tiles staged in LDS with 16-byte global loads, the
+//     products on the FP32 matrix cores (v_mfma_f32_32x32x2_f32), one LDS stage.
+//   DoubleBuffered: Vectorized with two LDS stages; the next tile's global
+//     loads are in flight while the current one is multiplied.
+//   SplitK: DoubleBuffered with K split over the grid's depth and a
+//     deterministic fixed-order reduction of the partial products.
+//   TensorCoreBf16 / TensorCoreF16: inputs rounded to nearest-even into
+//     bf16 / fp16 while they are staged in LDS, products on the bf16 / fp16
+//     matrix cores (v_mfma_f32_16x16x32_{bf16,f16}), FP32 accumulation, split-K
+//     where SplitK splits.
+//   TensorCoreTf32: gfx950 has no xf32 matrix instruction; compiling a graph
+//     with it fails, naming the kernel and the device.
+enum class MatmulKernel {
+    Auto,
+    Naive,
+    Tiled,
+    RegisterTiled128,
+    RegisterTiled64,
+    Vectorized,
+    DoubleBuffered,
+    SplitK,
+    TensorCoreTf32,
+    TensorCoreBf16,
+    TensorCoreF16,
+};
+
+const char* matmul_kernel_name(MatmulKernel kernel);
+Result<MatmulKernel> matmul_kernel_from_name(const std::string& name);
+
+// Auto becomes SplitK when split_k_splits() divides K for this shape on
+// `cu_count` CUs, DoubleBuffered otherwise; every other kernel is returned
+// unchanged (reference: cuda_backend.cpp:43-49).
+MatmulKernel resolve_matmul_kernel(MatmulKernel kernel, int m, int n, int k, int cu_count);
+
+struct HipOptions {
+    int device = 0;
+    MatmulKernel matmul = MatmulKernel::Auto;
+    // 16-byte loads and stores in elementwise kernels when the layout allows.
+    bool vectorize = true;
+};
+
+// What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).
+struct DeviceInfo {
+    std::string name;           // marketing name
+    std::string arch;           // gcnArchName, e.g. "gfx950:sramecc+:xnack-"
+    int cu_count = 0;
+    int wave_size = 0;
+    double clock_mhz = 0;       // max engine clock the runtime reports
+    double mem_clock_mhz = 0;
+    int bus_width_bits = 0;
+    std::size_t total_memory = 0;
+    std::size_t l2_bytes = 0;
+    std::size_t lds_bytes_per_block = 0;
+    int runtime_version = 0;
+    int driver_version = 0;
+
+    // Double data rate x memory clock x bus width.
+    double peak_bandwidth_gbs() const { return 2.0 * mem_clock_mhz * 1e6 * bus_width_bits / 8.0 / 1e9; }
+    // CDNA4 per CU and clock: 256 FP32 FLOP (matrix cores, or packed vector
+    // FMA), 4096 dense bf16/fp16 FLOP on the matrix cores.
+    double peak_fp32_gflops(double clock) const { return 256.0 * cu_count * clock * 1e6 / 1e9; }
+    double peak_bf16_gflops(double clock) const { return 4096.0 * cu_count * clock * 1e6 / 1e9; }
+};
+
+Result<DeviceInfo> query_device(int device = 0);
+
+// The engine clock right now in MHz, or 0 when the runtime cannot tell.
+double current_clock_mhz(int device = 0);
+
+// A graph compiled for the GPU. Every device allocation is one arena taken at
+// compile time: pooled intermediates and outputs at the memory plan's
+// offsets, graph inputs, constants (uploaded once) and split-K workspaces.
+class HipExecutable : public Executable {
+public:
+    // Copies host inputs into the arena; returns once they are resident.
+    virtual Status upload_inputs(const std::vector<const float*>& host_inputs) = 0;
+    // Launches every kernel in order on `stream` (a hipStream_t; nullptr: the
+    // executable's own stream). No copies, no synchronisation.
+    virtual Status enqueue(void* stream = nullptr) = 0;
+    // enqueue() with events[j] recorded before launch j and events[launches]
+    // after the last one (kernel_launches() + 1 hipEvent_t handles).
+    virtual Status enqueue_with_events(void* stream, void* const* events) = 0;
+    virtual Status synchronize() = 0;
+    // Waits for the device, then copies the outputs to the host.
+    virtual Status download_outputs(const std::vector<float*>& host_outputs) = 0;
+
+    // Caller-owned device memory for inputs / outputs (nullptr entries keep
+    // the arena's buffer). Bound outputs are written in place by the kernel
+    // that computes them, with no copy. Pointers must be 16-byte aligned.
+    virtual Status bind_inputs(const std::vector<const void*>& device_inputs) = 0;
+    virtual Status bind_outputs(const std::vector<void*>& device_outputs) = 0;
+    virtual void* input_device_ptr(std::size_t k) const = 0;
+    virtual void* output_device_ptr(std::size_t k) const = 0;
+    // The executable's own stream (a hipStream_t).
+    virtual void* stream() const = 0;
+
+    virtual std::size_t kernel_launches() const = 0;
+    virtual std::vector<std::string> kernel_sources() const = 0;
+    // One label per launch: "matmul <kernel> MxNxK" or "<op> <node> f32[...]".
+    virtual std::vector<std::string> launch_names() const = 0;
+    virtual std::vector<MatmulKernel> matmul_kernels() const = 0;
+    virtual double jit_compile_ms() const = 0;
+    virtual std::size_t arena_bytes() const = 0;
+};
+
+Result<std::unique_ptr<HipExecutable>> compile_for_hip(const Graph& graph, const HipOptions& options = {});
+Result<std::unique_ptr<Backend>> make_hip_backend(const HipOptions& options = {});
+
+}  // namespace minicompiler::hip

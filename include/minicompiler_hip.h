@@ -1,0 +1,180 @@
+/* minicompiler_hip.h - the C ABI of the MI355X (gfx950) backend for the
+ * minicompiler ML-graph compiler.
+ *
+ * One shared library, libminicompiler_hip.so, exports these functions with
+ * plain pointers and sizes only. Part 1 is exactly the reference's ctypes
+ * boundary (bench/capi.cpp), which its Python harness binds
+ * (bench/torch_compare.py); part 2 adds what this backend exposes beyond it:
+ * compiling from text, in-place device inputs/outputs, graph introspection,
+ * the GEMM operator (the reference's launch_matmul, matmul_kernels.hpp:36-59),
+ * the kernel generator (codegen.hpp:34-40) and the device memory, stream and
+ * event calls a caller needs to drive it without another runtime.
+ *
+ * Conventions: int-returning calls give 0 on success. Graph-level calls give
+ * 1 on failure and record a message readable with mc_last_error() (per
+ * thread). Device-level calls (mc_launch_*, mc_device_*, mc_memcpy_*, ...)
+ * return the hipError_t value; mc_error_string() describes it. Text-out
+ * calls write at most `size` bytes including the terminating NUL and return
+ * the full length of the text (like snprintf), or -1 on failure.
+ * Handles are not thread-safe; one handle, one thread at a time. */
+#ifndef MINICOMPILER_HIP_H
+#define MINICOMPILER_HIP_H
+
+#include <stddef.h>
+
+#if defined(__GNUC__)
+#define MC_API __attribute__((visibility("default")))
+#else
+#define MC_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Part 1: the reference's C interface (bench/capi.cpp) ---------------- */
+
+/* Parses the .mcg file `graph_path` with dim overrides `dims` ("M=64,N=4096"
+ * or ""), runs the pass pipeline `passes` ("default", "none" or a list such as
+ * "dne,fold") and compiles for `backend`: "hip" (this library's backend) or
+ * "none" (passes only; no device is touched, for inspection). Returns NULL and
+ * writes a message to `error` on failure. (capi.cpp:62-109) */
+MC_API void* mc_compile(const char* graph_path, const char* dims, const char* passes, const char* backend,
+                        char* error, int error_size);
+MC_API int mc_num_inputs(const void* handle);                   /* capi.cpp:111-113 */
+MC_API int mc_num_outputs(const void* handle);                  /* capi.cpp:115-117 */
+MC_API long long mc_output_elements(const void* handle, int k); /* capi.cpp:120-123 */
+/* Host buffers in graph order; uploads, runs and downloads. (capi.cpp:127-132) */
+MC_API int mc_run(void* handle, const float* const* inputs, float* const* outputs);
+/* Copies host inputs to the device, where they stay. (capi.cpp:136-147) */
+MC_API int mc_upload(void* handle, const float* const* inputs);
+/* Launches every kernel on `stream` (a hipStream_t; NULL: the executable's
+ * own stream). No copies, no synchronisation. (capi.cpp:150-158) */
+MC_API int mc_enqueue(void* handle, void* stream);
+/* Waits for the device, then copies outputs to host buffers. (capi.cpp:161-171) */
+MC_API int mc_download(void* handle, float* const* outputs);
+/* Kernel launches per mc_enqueue, -1 without an executable. (capi.cpp:174-182) */
+MC_API int mc_kernel_launches(void* handle);
+/* The matmul kernel of each matmul, comma-separated. (capi.cpp:186-202) */
+MC_API int mc_matmul_kernels(void* handle, char* out, int size);
+/* Engine clock in MHz as the runtime reports it, 0 without a device. (capi.cpp:204-210) */
+MC_API double mc_gpu_sm_clock_mhz(void);
+/* JSON description of device 0 (name, arch, CUs, clocks, bus, peaks) with the
+ * `clocks` samples summarised. 0 ok, 1 no device, 2 `out` too small.
+ * (capi.cpp:215-231) */
+MC_API int mc_gpu_device_json(const double* clocks, int n, char* out, int size);
+MC_API void mc_release(void* handle); /* capi.cpp:233-235 */
+
+/* ---- Part 2: extensions ---------------------------------------------------- */
+
+/* mc_compile from graph text, with backend options
+ * "matmul=NAME,vectorize=0|1,device=N" (NULL or "" for defaults). */
+MC_API void* mc_compile_source(const char* text, const char* dims, const char* passes, const char* backend,
+                               const char* options, char* error, int error_size);
+/* The message of this thread's last failed call. */
+MC_API int mc_last_error(char* out, int size);
+MC_API long long mc_input_elements(const void* handle, int k);
+
+/* Device-resident operation (HipExecutable, cuda_backend.hpp:88-104 in the
+ * reference, plus in-place binding). Bound pointers must be 16-byte aligned
+ * device memory holding the graph's element count; NULL entries keep the
+ * executable's own buffer. Bound outputs are written in place by the kernel
+ * that computes them. */
+MC_API int mc_bind_inputs(void* handle, const void* const* device_inputs);
+MC_API int mc_bind_outputs(void* handle, void* const* device_outputs);
+MC_API void* mc_input_device_ptr(void* handle, int k);
+MC_API void* mc_output_device_ptr(void* handle, int k);
+MC_API void* mc_stream(void* handle);
+MC_API int mc_synchronize(void* handle);
+MC_API double mc_jit_compile_ms(void* handle);
+MC_API long long mc_intermediate_bytes(void* handle);
+MC_API long long mc_arena_bytes(void* handle);
+
+/* Per-launch timing inside a timed region: mc_profile_start allocates HIP
+ * events for `steps` enqueues; each mc_enqueue_profiled then records an event
+ * before every launch and after the last one on `stream`; mc_profile_read
+ * waits and writes steps x kernel_launches durations in ms (step-major),
+ * returning their count. mc_launch_names lists the launches, one per line. */
+MC_API int mc_profile_start(void* handle, int steps);
+MC_API int mc_enqueue_profiled(void* handle, void* stream);
+MC_API int mc_profile_read(void* handle, float* ms, int capacity);
+MC_API int mc_launch_names(void* handle, char* out, int size);
+
+/* The library's seeded generators (random.hpp; fill_uniform is the
+ * reference's src/random.cpp:15-26), for callers that build inputs. */
+MC_API void mc_fill_uniform(float* out, size_t count, unsigned long long seed, float lo, float hi);
+MC_API void mc_fill_normal(float* out, size_t count, unsigned long long seed, double mean, double stddev);
+
+/* Introspection of the compiled graph (after the pipeline). */
+/* {"name":..,"nodes":[{"id","op","name","inputs","shape","program"?}],"inputs":[..],"outputs":[..]} */
+MC_API int mc_graph_json(const void* handle, char* out, int size);
+/* Copies the payload of constant node `node` (count elements). */
+MC_API int mc_constant_values(const void* handle, int node, float* out, long long count);
+/* Node and op counts after each pipeline stage (input first). */
+MC_API int mc_stage_stats_json(const void* handle, char* out, int size);
+/* The memory plan: buffer per node, buffer sizes, last uses. */
+MC_API int mc_plan_json(const void* handle, int pool_outputs, char* out, int size);
+/* Generated HIP source of every elementwise node, in launch order, separated
+ * by a line "//----". Works without a device. */
+MC_API int mc_kernel_sources(const void* handle, char* out, int size);
+/* The graph as `mcc --print` shows it. */
+MC_API int mc_print_graph(const void* handle, char* out, int size);
+
+/* The kernel generator (codegen.hpp:34-40): `program` in the printed form,
+ * one instruction per line ("r0 = load in0", "r1 = imm 0x3f000000" (bits) or
+ * "r1 = imm 0.5", "r2 = mul r0, r1"); `input_shapes` as "[8,64];[64];[]";
+ * `out_shape` as "[8,64]". *vectorized receives 1 for 16-byte accesses. */
+MC_API int mc_generate_elementwise_kernel(const char* program, const char* input_shapes, const char* out_shape,
+                                          int allow_vectorize, int items_per_lane, int* vectorized, char* out,
+                                          int size);
+/* hipRTC-compiles `source` for `arch` (e.g. "gfx950") to a code object with
+ * the generator's options; no device needed. Returns 0 or 1; the log goes to
+ * `log`. */
+MC_API int mc_compile_kernel_source(const char* source, const char* arch, char* log, int log_size);
+
+/* The GEMM operator (launch_matmul, matmul_kernels.hpp:36-59): C[m,n] =
+ * A[m,k] B[k,n] row-major fp32 on `stream`. `kernel` is a MatmulKernel value
+ * (mc_matmul_kernel_from_name); Auto must be resolved first
+ * (mc_resolve_matmul_kernel). Kernels that split K read `splits` and, above
+ * 1, `workspace` (mc_matmul_workspace_bytes). Returns a hipError_t value. */
+MC_API int mc_launch_matmul(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
+                            int splits, float* workspace);
+/* The matrix-core kernels on inputs already stored as bf16 (dtype 1) or fp16
+ * (dtype 2); fp32 accumulation and output. */
+MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,
+                                 void* stream, int splits, float* workspace);
+/* fp32 to bf16 (dtype 1) / fp16 (dtype 2), round to nearest even. */
+MC_API int mc_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream);
+/* c = sum of `splits` partials of `count` floats, fixed order (matmul_kernels.hpp:53-59). */
+MC_API int mc_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
+MC_API int mc_split_k_splits(int m, int n, int k, int cu_count, int blocks_per_cu); /* matmul_kernels.hpp:11-17 */
+MC_API int mc_matmul_splits(int kernel, int m, int n, int k, int cu_count);         /* matmul_kernels.hpp:23-25 */
+MC_API long long mc_matmul_workspace_bytes(int kernel, int m, int n, int splits);   /* matmul_kernels.hpp:27-30 */
+MC_API int mc_resolve_matmul_kernel(int kernel, int m, int n, int k, int cu_count); /* cuda_backend.hpp:45-49 */
+MC_API const char* mc_matmul_kernel_name(int kernel);                               /* cuda_backend.hpp:39 */
+MC_API int mc_matmul_kernel_from_name(const char* name); /* -1 if unknown (cuda_backend.hpp:41-43) */
+MC_API int mc_matmul_supported(int kernel);              /* tensor_core_supported, matmul_kernels.hpp:39-43 */
+
+/* Device memory, streams and events (the thin layer, for callers with no
+ * other HIP runtime in the process). */
+MC_API int mc_device_count(void);
+MC_API int mc_device_malloc(void** ptr, size_t bytes);
+MC_API int mc_device_free(void* ptr);
+MC_API int mc_memcpy_htod(void* dst, const void* src, size_t bytes);
+MC_API int mc_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+MC_API int mc_memset(void* dst, int value, size_t bytes);
+MC_API int mc_device_synchronize(void);
+MC_API int mc_stream_create(void** stream);
+MC_API int mc_stream_destroy(void* stream);
+MC_API int mc_stream_synchronize(void* stream);
+MC_API int mc_event_create(void** event);
+MC_API int mc_event_destroy(void* event);
+MC_API int mc_event_record(void* event, void* stream);
+MC_API int mc_event_elapsed_ms(void* start, void* stop, float* ms);
+MC_API const char* mc_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINICOMPILER_HIP_H */

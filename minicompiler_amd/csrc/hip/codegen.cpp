@@ -1,0 +1,254 @@
+// HIP C++ generator for elementwise kernels on gfx950 (replaces the
+// reference's src/cuda/codegen.cpp:14-182; the access classes and the
+// vectorisation rule are the reference's, the kernel shape is CDNA4's).
+//
+// Kernel shape. A block is 256 lanes (four wave64s). Each lane owns
+// `items_per_lane` items (16-byte vectors when vectorised) spaced one block
+// apart, so every load instruction of a wave reads 1 KiB of consecutive
+// memory. A lane issues all its loads, then evaluates the program per float,
+// then issues all its stores: U x 16 bytes in flight per lane. The grid
+// walks the tensor in block-sized steps of 256 x U items; steps where a lane's
+// items are all in range take the unchecked path, the single ragged step the
+// checked one.
+//
+// Numerics. The program is a device function of the inputs' floats: one
+// `const float` per instruction, so with -ffp-contract=off every op rounds
+// to float, as the reference's per-instruction register semantics require.
+// Immediates are written as their exact bit patterns.
+
+#include "codegen.hpp"
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <sstream>
+
+namespace minicompiler::hip {
+
+namespace {
+
+std::string exact_float(float v) {
+    std::uint32_t bits = 0;
+    std::memcpy(&bits, &v, sizeof bits);
+    char buf[96];
+    std::snprintf(buf, sizeof buf, "__uint_as_float(0x%08xu) /* %.9g */", static_cast<unsigned>(bits),
+                  static_cast<double>(v));
+    return buf;
+}
+
+std::string op_text(OpKind op, const std::string& a, const std::string& b) {
+    switch (op) {
+        case OpKind::Neg: return "-" + a;
+        case OpKind::Exp: return "expf(" + a + ")";
+        case OpKind::Log: return "logf(" + a + ")";
+        case OpKind::Sqrt: return "sqrtf(" + a + ")";
+        case OpKind::Relu: return "fmaxf(" + a + ", 0.0f)";
+        case OpKind::Sigmoid: return "1.0f / (1.0f + expf(-" + a + "))";
+        case OpKind::Tanh: return "tanhf(" + a + ")";
+        case OpKind::Add: return a + " + " + b;
+        case OpKind::Sub: return a + " - " + b;
+        case OpKind::Mul: return a + " * " + b;
+        case OpKind::Div: return a + " / " + b;
+        default: return "__builtin_nanf(\"\") /* not an elementwise op */";
+    }
+}
+
+std::string u32(std::size_t v) { return std::to_string(v) + "u"; }
+
+}  // namespace
+
+Access classify_access(const Shape& in, const Shape& out) {
+    const std::size_t count = num_elements(in);
+    if (count == 1) return {Access::Kind::Scalar, 0, ""};
+    if (count == num_elements(out)) return {Access::Kind::Contiguous, 0, ""};
+    // Leading 1s dropped, the rest equal to the output's trailing dims: the
+    // input repeats every `count` output elements.
+    std::size_t lead = 0;
+    while (lead < in.size() && in[lead] == 1) ++lead;
+    const std::size_t rest = in.size() - lead;
+    if (rest <= out.size() && std::equal(in.begin() + static_cast<std::ptrdiff_t>(lead), in.end(),
+                                         out.end() - static_cast<std::ptrdiff_t>(rest))) {
+        return {Access::Kind::Periodic, count, ""};
+    }
+    // sum over broadcast-free dims d of coord_d * stride_d, with
+    // coord_d = (i / out_stride_d) % out_d (the outermost never wraps).
+    const std::vector<std::int64_t> strides = broadcast_strides(in, out);
+    std::vector<std::size_t> out_stride(out.size());
+    std::size_t s = 1;
+    for (std::size_t d = out.size(); d-- > 0;) {
+        out_stride[d] = s;
+        s *= static_cast<std::size_t>(out[d]);
+    }
+    std::string expr;
+    for (std::size_t d = 0; d < out.size(); ++d) {
+        if (strides[d] == 0) continue;
+        std::string coord = out_stride[d] == 1 ? "i" : "(i / " + u32(out_stride[d]) + ")";
+        if (d > 0) coord = "(" + coord + " % " + u32(static_cast<std::size_t>(out[d])) + ")";
+        if (strides[d] != 1) coord += " * " + u32(static_cast<std::size_t>(strides[d]));
+        expr += (expr.empty() ? "" : " + ") + coord;
+    }
+    return {Access::Kind::General, 0, expr};
+}
+
+FusedProgram single_op_program(OpKind op) {
+    FusedProgram p;
+    if (is_unary_elementwise(op)) {
+        p.instrs = {FusedInstr::load(0), FusedInstr::unary(op, 0)};
+    } else {
+        p.instrs = {FusedInstr::load(0), FusedInstr::load(1), FusedInstr::binary(op, 0, 1)};
+    }
+    p.source_nodes = {op_name(op)};
+    return p;
+}
+
+ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const std::vector<Shape>& input_shapes,
+                                              const Shape& out_shape, const CodegenOptions& options) {
+    const std::size_t num_inputs = input_shapes.size();
+    std::vector<Access> access;
+    access.reserve(num_inputs);
+    for (const Shape& s : input_shapes) access.push_back(classify_access(s, out_shape));
+
+    // 16-byte vectors when the element count is a multiple of 4 and no input
+    // needs per-element index math; a periodic input must repeat on a
+    // vector boundary (reference rule, codegen.cpp:102-106).
+    bool vec = options.allow_vectorize && num_elements(out_shape) % 4 == 0;
+    for (const Access& a : access) {
+        if (a.kind == Access::Kind::General) vec = false;
+        if (a.kind == Access::Kind::Periodic && a.period % 4 != 0) vec = false;
+    }
+    const unsigned per_lane = std::max(1u, options.items_per_lane);
+    const std::string item = vec ? "mc_f32x4" : "float";
+
+    std::ostringstream os;
+    os << "// minicompiler-hip elementwise kernel: " << program.num_ops() << " op(s), out f32"
+       << to_string(out_shape) << ", " << (vec ? "16-byte vector accesses" : "scalar accesses") << ", " << per_lane
+       << " item(s) per lane per step.\n";
+    os << "typedef float mc_f32x4 __attribute__((ext_vector_type(4)));\n\n";
+
+    // The program: one argument per fused input (its element, or its scalar).
+    os << "__device__ __forceinline__ float mc_program(";
+    for (std::size_t k = 0; k < num_inputs; ++k) os << (k ? ", " : "") << "float x" << k;
+    if (num_inputs == 0) os << "void";
+    os << ")\n{\n";
+    for (std::size_t r = 0; r < program.instrs.size(); ++r) {
+        const FusedInstr& ins = program.instrs[r];
+        os << "\tconst float r" << r << " = ";
+        switch (ins.kind) {
+            case FusedInstr::Kind::Load: os << "x" << ins.a; break;
+            case FusedInstr::Kind::Immediate: os << exact_float(ins.immediate); break;
+            case FusedInstr::Kind::Unary: os << op_text(ins.op, "r" + std::to_string(ins.a), ""); break;
+            case FusedInstr::Kind::Binary:
+                os << op_text(ins.op, "r" + std::to_string(ins.a), "r" + std::to_string(ins.b));
+                break;
+        }
+        os << ";\n";
+    }
+    os << "\treturn r" << program.instrs.size() - 1 << ";\n}\n\n";
+
+    // Loads and stores.
+    const std::string ld_open = options.nontemporal_loads ? "__builtin_nontemporal_load(&" : "(";
+    const std::string st_prefix = options.nontemporal_stores ? "__builtin_nontemporal_store(" : "";
+
+    os << "extern \"C\" __global__ void __launch_bounds__(" << kElementwiseBlock << ")\n"
+       << kElementwiseKernelName << "(float* __restrict__ out";
+    for (std::size_t k = 0; k < num_inputs; ++k) os << ", const float* __restrict__ in" << k;
+    os << ", unsigned n)\n{\n";
+
+    for (std::size_t k = 0; k < num_inputs; ++k) {
+        if (access[k].kind == Access::Kind::Scalar) os << "\tconst float s" << k << " = in" << k << "[0];\n";
+    }
+    const std::string B = u32(kElementwiseBlock);
+    const std::string step = u32(static_cast<std::size_t>(kElementwiseBlock) * per_lane);
+    os << "\tconst unsigned step = gridDim.x * " << step << ";\n";
+    os << "\tunsigned i = blockIdx.x * " << step << " + threadIdx.x;\n";
+
+    // Index of item `u` of this lane for input k.
+    auto index_of = [&](std::size_t k, const std::string& pos) -> std::string {
+        const Access& a = access[k];
+        if (a.kind == Access::Kind::Contiguous) return pos;
+        if (a.kind == Access::Kind::Periodic) {
+            return "(" + pos + ") % " + u32(vec ? a.period / 4 : a.period);
+        }
+        // General: the expression is in terms of `i`; bind it to this position.
+        return "mc_general_" + std::to_string(k) + "(" + pos + ")";
+    };
+    std::ostringstream helpers;
+    for (std::size_t k = 0; k < num_inputs; ++k) {
+        if (access[k].kind == Access::Kind::General) {
+            helpers << "__device__ __forceinline__ unsigned mc_general_" << k << "(unsigned i) { return "
+                    << access[k].index << "; }\n";
+        }
+    }
+
+    auto load_expr = [&](std::size_t k, const std::string& pos) {
+        const std::string ptr = vec ? "reinterpret_cast<const mc_f32x4*>(in" + std::to_string(k) + ")"
+                                    : "in" + std::to_string(k);
+        return ld_open + ptr + "[" + index_of(k, pos) + "])";
+    };
+    // The program over one float lane of every input's item u.
+    auto call = [&](const std::string& lane) {
+        std::string c = "mc_program(";
+        for (std::size_t k = 0; k < num_inputs; ++k) {
+            if (k) c += ", ";
+            c += access[k].kind == Access::Kind::Scalar ? "s" + std::to_string(k)
+                                                        : "a" + std::to_string(k) + "[u]" + lane;
+        }
+        return c + ")";
+    };
+    auto store_stmt = [&](const std::string& pos, const std::string& value) {
+        const std::string ptr = vec ? "reinterpret_cast<" + item + "*>(out)" : "out";
+        if (options.nontemporal_stores) return st_prefix + value + ", &" + ptr + "[" + pos + "]);";
+        return ptr + "[" + pos + "] = " + value + ";";
+    };
+    auto emit_step = [&](const std::string& indent, bool checked) {
+        for (std::size_t k = 0; k < num_inputs; ++k) {
+            if (access[k].kind == Access::Kind::Scalar) continue;
+            os << indent << item << " a" << k << "[" << per_lane << "];\n";
+        }
+        os << indent << "#pragma unroll\n" << indent << "for (unsigned u = 0; u < " << per_lane << "u; ++u) {\n";
+        os << indent << "\tconst unsigned p = i + u * " << B << ";\n";
+        if (checked) os << indent << "\tif (p >= n) break;\n";
+        for (std::size_t k = 0; k < num_inputs; ++k) {
+            if (access[k].kind == Access::Kind::Scalar) continue;
+            os << indent << "\ta" << k << "[u] = " << load_expr(k, "p") << ";\n";
+        }
+        os << indent << "}\n";
+        os << indent << "#pragma unroll\n" << indent << "for (unsigned u = 0; u < " << per_lane << "u; ++u) {\n";
+        os << indent << "\tconst unsigned p = i + u * " << B << ";\n";
+        if (checked) os << indent << "\tif (p >= n) break;\n";
+        if (vec) {
+            os << indent << "\tmc_f32x4 o;\n";
+            for (const char* lane : {".x", ".y", ".z", ".w"}) {
+                os << indent << "\to" << lane << " = " << call(lane) << ";\n";
+            }
+            os << indent << "\t" << store_stmt("p", "o") << "\n";
+        } else {
+            os << indent << "\t" << store_stmt("p", call("")) << "\n";
+        }
+        os << indent << "}\n";
+    };
+
+    // Steps where all of this lane's items are in range.
+    os << "\tfor (; i + " << u32(static_cast<std::size_t>(kElementwiseBlock) * (per_lane - 1)) << " < n; i += step) {\n";
+    emit_step("\t\t", false);
+    os << "\t}\n";
+    // At most one ragged step remains for this lane.
+    os << "\tif (i < n) {\n";
+    emit_step("\t\t", true);
+    os << "\t}\n}\n";
+
+    // General-access index helpers go in front of the kernel.
+    std::string text = os.str();
+    if (!helpers.str().empty()) {
+        const std::size_t kernel_at = text.find("extern \"C\" __global__");
+        text.insert(kernel_at, helpers.str() + "\n");
+    }
+    ElementwiseKernel k;
+    k.source = std::move(text);
+    k.vectorized = vec;
+    k.items_per_lane = per_lane;
+    return k;
+}
+
+}  // namespace minicompiler::hip

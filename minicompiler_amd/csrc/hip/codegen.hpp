@@ -1,0 +1,69 @@
+#pragma once
+
+// Generates gfx950 HIP C++ for one elementwise node (a fused program, or a
+// single op wrapped as one). Plain C++ with no HIP headers, so it is built
+// and tested without a GPU. It takes the place of the reference's
+// src/cuda/codegen.hpp:15-40 with the same contract:
+//
+//   extern "C" __global__ void mc_elementwise(float* out, const float* in0, ..., unsigned n)
+//
+// where `n` counts 16-byte vectors of 4 floats when the kernel is vectorised
+// and single floats otherwise. Shapes are known when the graph is compiled,
+// so broadcast index math uses constant divisors, immediates are exact bit
+// patterns, and scalar inputs are loaded once per lane before the loop.
+
+#include "minicompiler/fused_program.hpp"
+#include "minicompiler/tensor.hpp"
+
+#include <cstddef>
+#include <string>
+#include <vector>
+
+namespace minicompiler::hip {
+
+inline constexpr const char* kElementwiseKernelName = "mc_elementwise";
+// Lanes per block: four 64-wide waves. The generated kernel assumes it.
+inline constexpr unsigned kElementwiseBlock = 256;
+
+struct CodegenOptions {
+    // 16-byte accesses when every input allows them.
+    bool allow_vectorize = true;
+    // Vectors (or floats) each lane loads before it computes and stores: more
+    // bytes in flight per wave to cover HBM latency.
+    unsigned items_per_lane = 4;
+    // Non-temporal hints on the streaming loads and stores.
+    bool nontemporal_loads = false;
+    bool nontemporal_stores = true;
+};
+
+struct ElementwiseKernel {
+    std::string source;
+    bool vectorized = false;
+    unsigned items_per_lane = 1;
+    // Elements (or vectors) one block covers per step of its loop.
+    unsigned items_per_block_step() const { return kElementwiseBlock * items_per_lane; }
+};
+
+// How the kernel reads one input of shape `in` for an output of shape `out`.
+struct Access {
+    enum class Kind {
+        Contiguous,  // same element count as the output: element i
+        Scalar,      // one element, loaded before the loop
+        Periodic,    // a suffix of the output shape (a bias row): element i % period
+        General,     // anything else: index expression with constant divisors
+    };
+    Kind kind = Kind::Contiguous;
+    std::size_t period = 0;
+    std::string index;  // General: expression in `i`
+};
+
+Access classify_access(const Shape& in, const Shape& out);
+
+ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const std::vector<Shape>& input_shapes,
+                                              const Shape& out_shape, const CodegenOptions& options = {});
+
+// One unary or binary op as a program (load the operands, apply the op), so
+// unfused graphs go through the same generator.
+FusedProgram single_op_program(OpKind op);
+
+}  // namespace minicompiler::hip

@@ -1,0 +1,456 @@
+// The HIP executable and backend (replaces the reference's
+// src/cuda/cuda_backend.cpp:52-366).
+//
+// Compile time (init): plan memory, lay every device allocation out in ONE
+// arena (pooled plan buffers at their plan offsets, graph inputs, constants
+// uploaded once, split-K workspaces; 256-byte aligned), generate and
+// hipRTC-compile one kernel per elementwise node (concurrently), and build a
+// flat launch list whose kernel arguments point at stable storage.
+// Run time: enqueue() walks the list; no allocation, no host work beyond the
+// launch calls. Inputs and outputs can be bound to caller device memory, in
+// which case the kernels read and write it in place.
+
+#include "minicompiler/hip/hip_backend.hpp"
+
+#include "codegen.hpp"
+#include "hip_rt.h"
+#include "kernel_compiler.hpp"
+#include "matmul.h"
+#include "matmul_policy.hpp"
+#include "minicompiler/runtime/memory_plan.hpp"
+
+#include <algorithm>
+#include <atomic>
+#include <cstdint>
+#include <thread>
+
+namespace minicompiler::hip {
+
+namespace {
+
+constexpr std::size_t kArenaAlign = 256;
+
+std::size_t align_up(std::size_t v) { return (v + kArenaAlign - 1) / kArenaAlign * kArenaAlign; }
+
+Status hip_status(int rc, const char* call) {
+    if (rc == 0) return Status();
+    return Error{std::string(call) + ": " + mchip_error_string(rc)};
+}
+
+#define MCHIP_TRY(call)                                  \
+    do {                                                 \
+        const int mchip_rc_ = (call);                    \
+        if (mchip_rc_ != 0) return hip_status(mchip_rc_, #call); \
+    } while (0)
+
+bool is_tensor_core(MatmulKernel k) {
+    return k == MatmulKernel::TensorCoreTf32 || k == MatmulKernel::TensorCoreBf16 || k == MatmulKernel::TensorCoreF16;
+}
+
+std::string arch_base(const std::string& arch) { return arch.substr(0, arch.find(':')); }
+
+struct Launch {
+    enum class Kind { Elementwise, Matmul } kind = Kind::Elementwise;
+    NodeId node = kNoNode;
+    // Elementwise: generated kernel, arguments out, in0.., count.
+    void* function = nullptr;
+    unsigned grid = 0;
+    unsigned count = 0;
+    std::vector<void*> ptrs;
+    std::vector<void*> params;
+    // Matmul.
+    MatmulKernel matmul = MatmulKernel::DoubleBuffered;
+    int splits = 1;
+    float* workspace = nullptr;
+    int m = 0, n = 0, k = 0;
+};
+
+class HipExecutableImpl final : public HipExecutable {
+public:
+    HipExecutableImpl(const Graph& graph, const HipOptions& options)
+        : graph_(graph), options_(options), plan_(plan_memory(graph_)) {}
+
+    ~HipExecutableImpl() override {
+        if (stream_) mchip_stream_destroy(stream_);
+        if (arena_) mchip_free(arena_);
+    }
+
+    Status init() {
+        Result<DeviceInfo> dev = query_device(options_.device);
+        if (!dev.ok()) return dev.error();
+        device_ = std::move(dev).value();
+        MCHIP_TRY(mchip_set_device(options_.device));
+        MCHIP_TRY(mchip_stream_create(&stream_));
+
+        const std::size_t n = graph_.num_nodes();
+        offset_.assign(n, 0);
+        bound_.assign(n, nullptr);
+
+        // Arena layout: plan buffers first, then inputs, constants, workspaces.
+        std::vector<std::size_t> buffer_offset(plan_.buffer_bytes.size());
+        std::size_t top = 0;
+        for (std::size_t b = 0; b < plan_.buffer_bytes.size(); ++b) {
+            buffer_offset[b] = top;
+            top += align_up(std::max<std::size_t>(plan_.buffer_bytes[b], 4));
+        }
+        for (std::size_t i = 0; i < n; ++i) {
+            const Node& node = graph_.node(static_cast<NodeId>(i));
+            if (node.op == OpKind::Input || node.op == OpKind::Constant) {
+                offset_[i] = top;
+                top += align_up(std::max<std::size_t>(node.type.size_bytes(), 4));
+            } else {
+                offset_[i] = buffer_offset[static_cast<std::size_t>(plan_.buffer_of[i])];
+            }
+        }
+
+        // Launches (matmul workspaces take arena space too).
+        std::vector<std::size_t> workspace_offset;
+        for (std::size_t i = 0; i < n; ++i) {
+            const auto id = static_cast<NodeId>(i);
+            const Node& node = graph_.node(id);
+            if (!is_compute(node.op)) continue;
+            Launch l;
+            l.node = id;
+            if (node.op == OpKind::MatMul) {
+                Status st = plan_matmul(node, &l);
+                if (!st.ok()) return st;
+                const std::size_t ws = matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
+                workspace_offset.push_back(ws ? top : SIZE_MAX);
+                if (ws) top += align_up(ws);
+            } else {
+                l.kind = Launch::Kind::Elementwise;
+                workspace_offset.push_back(SIZE_MAX);
+            }
+            launches_.push_back(std::move(l));
+        }
+        arena_bytes_ = std::max<std::size_t>(top, kArenaAlign);
+        MCHIP_TRY(mchip_malloc(&arena_, arena_bytes_));
+        auto* base = static_cast<char*>(arena_);
+        for (std::size_t j = 0; j < launches_.size(); ++j) {
+            if (workspace_offset[j] != SIZE_MAX) launches_[j].workspace = reinterpret_cast<float*>(base + workspace_offset[j]);
+        }
+        // Constants are uploaded once, here.
+        for (std::size_t i = 0; i < n; ++i) {
+            const Node& node = graph_.node(static_cast<NodeId>(i));
+            if (node.op != OpKind::Constant) continue;
+            MCHIP_TRY(mchip_memcpy_htod_async(base + offset_[i], node.constant->data(), node.type.size_bytes(), stream_));
+        }
+        MCHIP_TRY(mchip_stream_synchronize(stream_));
+
+        Status st = build_elementwise();
+        if (!st.ok()) return st;
+        refresh_pointers();
+        return Status();
+    }
+
+    // Executable
+
+    Status run(const std::vector<HostTensor>& inputs, std::vector<HostTensor>& outputs) override {
+        if (&inputs == &outputs) return Error{"run() needs separate input and output vectors"};
+        if (inputs.size() != graph_.inputs().size()) {
+            return Error{"expected " + std::to_string(graph_.inputs().size()) + " inputs, got " +
+                         std::to_string(inputs.size())};
+        }
+        std::vector<const float*> in;
+        for (std::size_t k = 0; k < inputs.size(); ++k) {
+            const Node& node = graph_.node(graph_.inputs()[k]);
+            if (inputs[k].type != node.type || inputs[k].data.size() != node.type.num_elements()) {
+                return Error{"input '" + node.name + "' should be " + to_string(node.type) + ", got " +
+                             to_string(inputs[k].type)};
+            }
+            in.push_back(inputs[k].data.data());
+        }
+        outputs.resize(graph_.outputs().size());
+        std::vector<float*> out;
+        for (std::size_t k = 0; k < outputs.size(); ++k) {
+            const TensorType& t = graph_.node(graph_.outputs()[k]).type;
+            outputs[k].type = t;
+            outputs[k].data.resize(t.num_elements());
+            out.push_back(outputs[k].data.data());
+        }
+        return run_buffers(in, out);
+    }
+
+    Status run_buffers(const std::vector<const float*>& inputs, const std::vector<float*>& outputs) override {
+        if (inputs.size() != graph_.inputs().size() || outputs.size() != graph_.outputs().size()) {
+            return Error{"expected " + std::to_string(graph_.inputs().size()) + " input and " +
+                         std::to_string(graph_.outputs().size()) + " output buffers"};
+        }
+        Status st = upload_inputs(inputs);
+        if (st.ok()) st = enqueue(nullptr);
+        if (st.ok()) st = download_outputs(outputs);
+        return st;
+    }
+
+    std::size_t intermediate_bytes() const override { return plan_.bytes_with_reuse(); }
+
+    // HipExecutable
+
+    Status upload_inputs(const std::vector<const float*>& host_inputs) override {
+        if (host_inputs.size() != graph_.inputs().size()) return Error{"wrong number of inputs"};
+        MCHIP_TRY(mchip_set_device(options_.device));
+        for (std::size_t k = 0; k < host_inputs.size(); ++k) {
+            const NodeId id = graph_.inputs()[k];
+            MCHIP_TRY(mchip_memcpy_htod_async(value_ptr(id), host_inputs[k], graph_.node(id).type.size_bytes(), stream_));
+        }
+        // Kernels may be enqueued on another stream, which would not wait.
+        MCHIP_TRY(mchip_stream_synchronize(stream_));
+        return Status();
+    }
+
+    Status enqueue(void* stream) override { return enqueue_with_events(stream, nullptr); }
+
+    Status enqueue_with_events(void* stream, void* const* events) override {
+        void* s = stream ? stream : stream_;
+        std::size_t j = 0;
+        for (Launch& l : launches_) {
+            if (events) MCHIP_TRY(mchip_event_record(events[j++], s));
+            if (l.kind == Launch::Kind::Elementwise) {
+                const int rc = mchip_module_launch(l.function, l.grid, kElementwiseBlock, 0, s, l.params.data());
+                if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel");
+            } else {
+                const int rc = mchip_launch_matmul(static_cast<int>(l.matmul), static_cast<const float*>(value_ptr(a_of(l))),
+                                                   static_cast<const float*>(value_ptr(b_of(l))),
+                                                   static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, l.splits,
+                                                   l.workspace);
+                if (rc != 0) {
+                    return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " +
+                                 mchip_error_string(rc)};
+                }
+            }
+        }
+        if (events) MCHIP_TRY(mchip_event_record(events[j], s));
+        // Graph outputs that are inputs or constants: copy into bound memory.
+        for (std::size_t k = 0; k < graph_.outputs().size(); ++k) {
+            const NodeId id = graph_.outputs()[k];
+            if (is_compute(graph_.node(id).op) || output_bound_[k] == nullptr) continue;
+            MCHIP_TRY(mchip_memcpy_dtod_async(output_bound_[k], value_ptr(id), graph_.node(id).type.size_bytes(), s));
+        }
+        return Status();
+    }
+
+    Status synchronize() override {
+        MCHIP_TRY(mchip_set_device(options_.device));
+        MCHIP_TRY(mchip_device_synchronize());
+        return Status();
+    }
+
+    Status download_outputs(const std::vector<float*>& host_outputs) override {
+        if (host_outputs.size() != graph_.outputs().size()) return Error{"wrong number of outputs"};
+        MCHIP_TRY(mchip_set_device(options_.device));
+        // Kernels may have gone to a caller's stream: wait for the device.
+        MCHIP_TRY(mchip_device_synchronize());
+        for (std::size_t k = 0; k < host_outputs.size(); ++k) {
+            const NodeId id = graph_.outputs()[k];
+            const void* src = output_bound_[k] ? output_bound_[k] : value_ptr(id);
+            MCHIP_TRY(mchip_memcpy_dtoh(host_outputs[k], src, graph_.node(id).type.size_bytes()));
+        }
+        return Status();
+    }
+
+    Status bind_inputs(const std::vector<const void*>& device_inputs) override {
+        if (device_inputs.size() != graph_.inputs().size()) return Error{"wrong number of inputs to bind"};
+        for (const void* p : device_inputs) {
+            if (reinterpret_cast<std::uintptr_t>(p) % 16 != 0) return Error{"bound inputs must be 16-byte aligned"};
+        }
+        for (std::size_t k = 0; k < device_inputs.size(); ++k) {
+            bound_[static_cast<std::size_t>(graph_.inputs()[k])] = const_cast<void*>(device_inputs[k]);
+        }
+        refresh_pointers();
+        return Status();
+    }
+
+    Status bind_outputs(const std::vector<void*>& device_outputs) override {
+        if (device_outputs.size() != graph_.outputs().size()) return Error{"wrong number of outputs to bind"};
+        for (void* p : device_outputs) {
+            if (reinterpret_cast<std::uintptr_t>(p) % 16 != 0) return Error{"bound outputs must be 16-byte aligned"};
+        }
+        for (std::size_t k = 0; k < device_outputs.size(); ++k) {
+            const NodeId id = graph_.outputs()[k];
+            output_bound_[k] = device_outputs[k];
+            if (is_compute(graph_.node(id).op)) bound_[static_cast<std::size_t>(id)] = device_outputs[k];
+        }
+        refresh_pointers();
+        return Status();
+    }
+
+    void* input_device_ptr(std::size_t k) const override {
+        return k < graph_.inputs().size() ? value_ptr(graph_.inputs()[k]) : nullptr;
+    }
+    void* output_device_ptr(std::size_t k) const override {
+        if (k >= graph_.outputs().size()) return nullptr;
+        return output_bound_[k] ? output_bound_[k] : value_ptr(graph_.outputs()[k]);
+    }
+
+    void* stream() const override { return stream_; }
+
+    std::size_t kernel_launches() const override { return launches_.size(); }
+    std::vector<std::string> kernel_sources() const override { return sources_; }
+    std::vector<std::string> launch_names() const override {
+        std::vector<std::string> names;
+        for (const Launch& l : launches_) {
+            const Node& node = graph_.node(l.node);
+            if (l.kind == Launch::Kind::Matmul) {
+                names.push_back(std::string("matmul ") + matmul_kernel_name(l.matmul) + " " + std::to_string(l.m) +
+                                "x" + std::to_string(l.n) + "x" + std::to_string(l.k) +
+                                (l.splits > 1 ? " splits=" + std::to_string(l.splits) : ""));
+            } else {
+                names.push_back(std::string(op_name(node.op)) + " " + node.name + " " + to_string(node.type));
+            }
+        }
+        return names;
+    }
+    std::vector<MatmulKernel> matmul_kernels() const override {
+        std::vector<MatmulKernel> ks;
+        for (const Launch& l : launches_) {
+            if (l.kind == Launch::Kind::Matmul) ks.push_back(l.matmul);
+        }
+        return ks;
+    }
+    double jit_compile_ms() const override { return jit_ms_; }
+    std::size_t arena_bytes() const override { return arena_bytes_; }
+
+private:
+    NodeId a_of(const Launch& l) const { return graph_.node(l.node).inputs[0]; }
+    NodeId b_of(const Launch& l) const { return graph_.node(l.node).inputs[1]; }
+
+    void* value_ptr(NodeId id) const {
+        const auto i = static_cast<std::size_t>(id);
+        if (bound_[i]) return bound_[i];
+        return static_cast<char*>(arena_) + offset_[i];
+    }
+
+    Status plan_matmul(const Node& node, Launch* l) {
+        const Shape& a = graph_.node(node.inputs[0]).type.shape;
+        l->kind = Launch::Kind::Matmul;
+        l->m = static_cast<int>(a[0]);
+        l->k = static_cast<int>(a[1]);
+        l->n = static_cast<int>(node.type.shape[1]);
+        l->matmul = resolve_matmul_kernel(options_.matmul, l->m, l->n, l->k, device_.cu_count);
+        if (is_tensor_core(l->matmul) && !mchip_matmul_supported(static_cast<int>(l->matmul))) {
+            return Error{std::string("matmul kernel '") + matmul_kernel_name(l->matmul) + "' does not run on " +
+                         device_.name + " (" + device_.arch +
+                         "): gfx950 has bf16 and fp16 matrix instructions but no xf32 (TF32) one"};
+        }
+        l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
+        return Status();
+    }
+
+    // Generates every elementwise kernel and compiles them concurrently.
+    Status build_elementwise() {
+        struct Job {
+            std::size_t launch;
+            ElementwiseKernel kernel;
+        };
+        std::vector<Job> jobs;
+        CodegenOptions cg;
+        cg.allow_vectorize = options_.vectorize;
+        for (std::size_t j = 0; j < launches_.size(); ++j) {
+            if (launches_[j].kind != Launch::Kind::Elementwise) continue;
+            const Node& node = graph_.node(launches_[j].node);
+            const FusedProgram program =
+                node.op == OpKind::FusedElementwise ? *node.fused : single_op_program(node.op);
+            std::vector<Shape> shapes;
+            for (NodeId in : node.inputs) shapes.push_back(graph_.node(in).type.shape);
+            jobs.push_back({j, generate_elementwise_kernel(program, shapes, node.type.shape, cg)});
+        }
+        const std::string arch = arch_base(device_.arch);
+        const int dev = options_.device;
+        std::vector<Result<CompiledKernel>> built(jobs.size(), Result<CompiledKernel>(Error{"not compiled"}));
+        std::vector<double> ms(jobs.size(), 0.0);
+        const std::size_t workers =
+            std::max<std::size_t>(1, std::min<std::size_t>(jobs.size(), std::min(16u, std::max(1u, std::thread::hardware_concurrency()))));
+        std::vector<std::thread> pool;
+        std::atomic<std::size_t> next{0};
+        for (std::size_t w = 0; w < workers; ++w) {
+            pool.emplace_back([&]() {
+                mchip_set_device(dev);  // per thread
+                for (std::size_t j = next++; j < jobs.size(); j = next++) {
+                    built[j] = KernelCompiler::instance().get(jobs[j].kernel.source, kElementwiseKernelName, arch, dev, &ms[j]);
+                }
+            });
+        }
+        for (std::thread& t : pool) t.join();
+        for (std::size_t j = 0; j < jobs.size(); ++j) {
+            if (!built[j].ok()) return built[j].error();
+            Launch& l = launches_[jobs[j].launch];
+            const ElementwiseKernel& kern = jobs[j].kernel;
+            jit_ms_ += ms[j];
+            sources_.push_back(kern.source);
+            const std::size_t numel = graph_.node(l.node).type.num_elements();
+            l.function = built[j]->function;
+            l.count = static_cast<unsigned>(kern.vectorized ? numel / 4 : numel);
+            int per_cu = 0;
+            MCHIP_TRY(mchip_occupancy(&per_cu, l.function, static_cast<int>(kElementwiseBlock), 0));
+            const std::size_t per_step = kern.items_per_block_step();
+            const std::size_t needed = (static_cast<std::size_t>(l.count) + per_step - 1) / per_step;
+            const std::size_t resident = std::max<std::size_t>(1, static_cast<std::size_t>(per_cu) * device_.cu_count);
+            l.grid = static_cast<unsigned>(std::max<std::size_t>(1, std::min(needed, resident)));
+            l.ptrs.assign(1 + graph_.node(l.node).inputs.size(), nullptr);
+        }
+        // Stable argument addresses: the launch list no longer changes.
+        for (Launch& l : launches_) {
+            if (l.kind != Launch::Kind::Elementwise) continue;
+            for (void*& p : l.ptrs) l.params.push_back(&p);
+            l.params.push_back(&l.count);
+        }
+        return Status();
+    }
+
+    void refresh_pointers() {
+        if (output_bound_.size() != graph_.outputs().size()) output_bound_.assign(graph_.outputs().size(), nullptr);
+        for (Launch& l : launches_) {
+            if (l.kind != Launch::Kind::Elementwise) continue;
+            const Node& node = graph_.node(l.node);
+            l.ptrs[0] = value_ptr(l.node);
+            for (std::size_t k = 0; k < node.inputs.size(); ++k) l.ptrs[k + 1] = value_ptr(node.inputs[k]);
+        }
+    }
+
+    Graph graph_;
+    HipOptions options_;
+    MemoryPlan plan_;
+    DeviceInfo device_;
+    void* stream_ = nullptr;
+    void* arena_ = nullptr;
+    std::size_t arena_bytes_ = 0;
+    std::vector<std::size_t> offset_;    // per node: arena offset
+    std::vector<void*> bound_;           // per node: caller device memory, or nullptr
+    std::vector<void*> output_bound_;    // per graph output
+    std::vector<Launch> launches_;
+    std::vector<std::string> sources_;
+    double jit_ms_ = 0.0;
+};
+
+class HipBackend final : public Backend {
+public:
+    explicit HipBackend(const HipOptions& options) : options_(options) {}
+    const char* name() const override { return "hip"; }
+    Result<std::unique_ptr<Executable>> compile(const Graph& graph) override {
+        Result<std::unique_ptr<HipExecutable>> exe = compile_for_hip(graph, options_);
+        if (!exe.ok()) return exe.error();
+        return std::unique_ptr<Executable>(std::move(exe).value());
+    }
+
+private:
+    HipOptions options_;
+};
+
+}  // namespace
+
+Result<std::unique_ptr<HipExecutable>> compile_for_hip(const Graph& graph, const HipOptions& options) {
+    Status st = graph.verify();
+    if (!st.ok()) return st.error();
+    auto exe = std::make_unique<HipExecutableImpl>(graph, options);
+    st = exe->init();
+    if (!st.ok()) return st.error();
+    return std::unique_ptr<HipExecutable>(std::move(exe));
+}
+
+Result<std::unique_ptr<Backend>> make_hip_backend(const HipOptions& options) {
+    Result<DeviceInfo> dev = query_device(options.device);
+    if (!dev.ok()) return Error{"no usable HIP device: " + dev.error().message};
+    return std::unique_ptr<Backend>(std::make_unique<HipBackend>(options));
+}
+
+}  // namespace minicompiler::hip

@@ -1,0 +1,131 @@
+#include "kernel_compiler.hpp"
+
+#include "hip_rt.h"
+
+#include <chrono>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <fstream>
+#include <sstream>
+
+namespace minicompiler::hip {
+
+namespace {
+
+std::uint64_t fnv1a64(const std::string& s) {
+    std::uint64_t h = 0xcbf29ce484222325ull;
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+std::string disk_cache_path(const std::string& key) {
+    const char* dir = std::getenv("MINICOMPILER_HIP_CACHE_DIR");
+    if (dir == nullptr || *dir == '\0') return {};
+    char name[64];
+    std::snprintf(name, sizeof name, "/mc_%016llx.co", static_cast<unsigned long long>(fnv1a64(key)));
+    return std::string(dir) + name;
+}
+
+bool read_file(const std::string& path, std::string* out) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) return false;
+    std::ostringstream s;
+    s << f.rdbuf();
+    *out = s.str();
+    return !out->empty();
+}
+
+void write_file_atomically(const std::string& path, const std::string& data) {
+    const std::string tmp = path + ".tmp" + std::to_string(reinterpret_cast<std::uintptr_t>(&data));
+    {
+        std::ofstream f(tmp, std::ios::binary);
+        if (!f) return;
+        f.write(data.data(), static_cast<std::streamsize>(data.size()));
+    }
+    std::rename(tmp.c_str(), path.c_str());
+}
+
+std::string cache_key(const std::string& arch, const std::string& source) {
+    std::string key = arch;
+    for (const std::string& o : KernelCompiler::options_for(arch)) key += '\n' + o;
+    return key + '\n' + source;
+}
+
+}  // namespace
+
+KernelCompiler& KernelCompiler::instance() {
+    static KernelCompiler compiler;
+    return compiler;
+}
+
+std::vector<std::string> KernelCompiler::options_for(const std::string& arch) {
+    return {"--offload-arch=" + arch, "-O3", "-std=c++17", "-ffp-contract=off",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+}
+
+Result<std::string> KernelCompiler::compile_code_object(const std::string& source, const std::string& arch,
+                                                        double* compile_ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const std::string key = cache_key(arch, source);
+    const std::string path = disk_cache_path(key);
+    std::string code;
+    if (!path.empty() && read_file(path, &code)) {
+        if (compile_ms) *compile_ms = 0.0;
+        return code;
+    }
+    const std::vector<std::string> opts = options_for(arch);
+    std::vector<const char*> argv;
+    for (const std::string& o : opts) argv.push_back(o.c_str());
+    char* image = nullptr;
+    char* log = nullptr;
+    std::size_t size = 0;
+    const int rc = mchip_rtc_compile(source.c_str(), "mc_generated.hip", argv.data(), static_cast<int>(argv.size()),
+                                     &image, &size, &log);
+    const std::string log_text = log ? log : "";
+    mchip_rtc_free(log);
+    if (rc != 0) {
+        mchip_rtc_free(image);
+        return Error{std::string("hipRTC could not compile a generated kernel (") + mchip_rtc_error_string(rc) +
+                     "):\n" + log_text + "\n" + source};
+    }
+    code.assign(image, size);
+    mchip_rtc_free(image);
+    if (!path.empty()) write_file_atomically(path, code);
+    if (compile_ms) {
+        *compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    }
+    return code;
+}
+
+Result<CompiledKernel> KernelCompiler::get(const std::string& source, const char* name, const std::string& arch,
+                                           int device, double* compile_ms) {
+    if (compile_ms) *compile_ms = 0.0;
+    const std::string key = std::to_string(device) + '\n' + cache_key(arch, source) + '\n' + name;
+    {
+        std::lock_guard<std::mutex> lock(mutex_);
+        const auto it = loaded_.find(key);
+        if (it != loaded_.end()) return it->second;
+    }
+    // Compile outside the lock so executables can build kernels concurrently.
+    Result<std::string> code = compile_code_object(source, arch, compile_ms);
+    if (!code.ok()) return code.error();
+    std::lock_guard<std::mutex> lock(mutex_);
+    const auto it = loaded_.find(key);
+    if (it != loaded_.end()) return it->second;
+    CompiledKernel k;
+    int rc = mchip_module_load(&k.module, code->data());
+    if (rc != 0) return Error{std::string("hipModuleLoadData: ") + mchip_error_string(rc)};
+    rc = mchip_module_function(&k.function, k.module, name);
+    if (rc != 0) {
+        mchip_module_unload(k.module);
+        return Error{std::string("hipModuleGetFunction(") + name + "): " + mchip_error_string(rc)};
+    }
+    loaded_.emplace(key, k);
+    return k;
+}
+
+}  // namespace minicompiler::hip

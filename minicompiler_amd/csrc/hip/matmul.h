@@ -1,0 +1,44 @@
+/* Launchers of the AOT-compiled gfx950 matmul kernels (matmul_fp32.hip,
+ * matmul_mfma16.hip). Plain C ABI: the host C++ calls them without HIP
+ * headers. `kernel` takes the values of minicompiler::hip::MatmulKernel.
+ * Each returns 0 or a hipError_t value: hipErrorInvalidValue (1) for an
+ * unresolved Auto, a bad shape or a missing workspace, hipErrorNotSupported
+ * (801) for a kernel gfx950 cannot run (TensorCoreTf32).
+ *
+ * Replaces the reference's launch_matmul / launch_tensor_core /
+ * sum_split_partials (src/cuda/matmul_kernels.hpp:36-59). */
+#pragma once
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MCHIP_DTYPE_F32 = 0, MCHIP_DTYPE_BF16 = 1, MCHIP_DTYPE_F16 = 2 };
+
+/* C[m,n] = A[m,k] B[k,n], row-major fp32. A kernel that splits K reads
+ * `splits` and, above 1, `workspace` (splits * m * n floats). */
+int mchip_launch_matmul(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
+                        int splits, float* workspace);
+
+/* The matrix-core kernels on inputs already in bf16 or fp16 in device memory
+ * (dtype MCHIP_DTYPE_BF16 / MCHIP_DTYPE_F16), fp32 accumulation and output. */
+int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,
+                             void* stream, int splits, float* workspace);
+
+/* C = sum over z of partial[z * count + i], added in z order. */
+int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
+
+/* Whether gfx950 runs `kernel` (all but TensorCoreTf32). */
+int mchip_matmul_supported(int kernel);
+
+/* Resident blocks per CU of the kernel that runs `kernel` (occupancy), or 1. */
+int mchip_matmul_blocks_per_cu(int kernel);
+
+/* Elementwise fp32 -> bf16/fp16 (round to nearest even), for staging. */
+int mchip_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,389 @@
+// FP32 matmul kernels for gfx950 (CDNA4), ahead-of-time compiled. They take
+// the place of the reference's FP32 ladder (src/cuda/matmul_kernels.cu:18-417).
+// C[m,n] = A[m,k] B[k,n], row-major fp32, any shape.
+//
+// The ladder, one step of optimisation each:
+//   naive              one output per lane, operands from global memory
+//   tiled              32x32 LDS tiles, one output per lane
+//   register_tiled_*   128x128 / 64x64 LDS tiles, 8x8 / 4x4 outputs per lane
+//   vectorized         128x128x32 tiles, 16-byte global loads, the products on
+//                      the FP32 matrix cores (v_mfma_f32_32x32x2_f32)
+//   double_buffered    vectorized with two LDS stages: the next tile's global
+//                      loads are in flight during the current tile's MFMAs
+//   split_k            double_buffered with K split over the grid's depth and
+//                      a fixed-order (deterministic) sum of the partials
+
+#include "matmul.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// MatmulKernel values (minicompiler/hip/hip_backend.hpp).
+enum Kernel {
+    kAuto = 0,
+    kNaive,
+    kTiled,
+    kRegisterTiled128,
+    kRegisterTiled64,
+    kVectorized,
+    kDoubleBuffered,
+    kSplitK,
+    kTensorCoreTf32,
+    kTensorCoreBf16,
+    kTensorCoreF16,
+};
+
+// ---------------------------------------------------------------- naive
+
+__global__ void __launch_bounds__(256) matmul_naive(const float* __restrict__ a, const float* __restrict__ b,
+                                                    float* __restrict__ c, int m, int n, int k) {
+    const int col = blockIdx.x * 16 + threadIdx.x;
+    const int row = blockIdx.y * 16 + threadIdx.y;
+    if (row >= m || col >= n) return;
+    float acc = 0.0f;
+    const float* ar = a + static_cast<std::ptrdiff_t>(row) * k;
+    for (int t = 0; t < k; ++t) acc += ar[t] * b[static_cast<std::ptrdiff_t>(t) * n + col];
+    c[static_cast<std::ptrdiff_t>(row) * n + col] = acc;
+}
+
+// ---------------------------------------------------------------- tiled
+
+constexpr int kTile = 32;
+
+__global__ void __launch_bounds__(1024) matmul_tiled(const float* __restrict__ a, const float* __restrict__ b,
+                                                     float* __restrict__ c, int m, int n, int k) {
+    __shared__ float at[kTile][kTile + 1];
+    __shared__ float bt[kTile][kTile + 1];
+    const int tx = threadIdx.x, ty = threadIdx.y;
+    const int row = blockIdx.y * kTile + ty, col = blockIdx.x * kTile + tx;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < k; k0 += kTile) {
+        at[ty][tx] = (row < m && k0 + tx < k) ? a[static_cast<std::ptrdiff_t>(row) * k + k0 + tx] : 0.0f;
+        bt[ty][tx] = (k0 + ty < k && col < n) ? b[static_cast<std::ptrdiff_t>(k0 + ty) * n + col] : 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < kTile; ++t) acc += at[ty][t] * bt[t][tx];
+        __syncthreads();
+    }
+    if (row < m && col < n) c[static_cast<std::ptrdiff_t>(row) * n + col] = acc;
+}
+
+// ---------------------------------------------------------------- register tiled
+//
+// 256 lanes as an R x C grid (R = BM/TM, C = BN/TN). Lane (r, c) owns rows
+// r + R*i and columns c + C*j of the block tile: along a wave the B reads are
+// consecutive words and the A reads broadcasts. A is staged transposed (k
+// major) so both operands are read along a row of LDS.
+
+template <int BM, int BN, int BK, int TM, int TN>
+__global__ void __launch_bounds__(256) matmul_register_tiled(const float* __restrict__ a, const float* __restrict__ b,
+                                                             float* __restrict__ c, int m, int n, int k) {
+    constexpr int R = BM / TM, C = BN / TN;
+    static_assert(R * C == 256, "256 lanes");
+    __shared__ float as[BK][BM];
+    __shared__ float bs[BK][BN];
+    const int tid = threadIdx.x;
+    const int lr = tid / C, lc = tid % C;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    float acc[TM][TN] = {};
+    for (int k0 = 0; k0 < k; k0 += BK) {
+        for (int e = tid; e < BM * BK; e += 256) {
+            const int r = e / BK, kk = e % BK;
+            const int gr = row0 + r, gk = k0 + kk;
+            as[kk][r] = (gr < m && gk < k) ? a[static_cast<std::ptrdiff_t>(gr) * k + gk] : 0.0f;
+        }
+        for (int e = tid; e < BK * BN; e += 256) {
+            const int kk = e / BN, cc = e % BN;
+            const int gk = k0 + kk, gc = col0 + cc;
+            bs[kk][cc] = (gk < k && gc < n) ? b[static_cast<std::ptrdiff_t>(gk) * n + gc] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < BK; ++t) {
+            float av[TM], bv[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) av[i] = as[t][lr + R * i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bv[j] = bs[t][lc + C * j];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] += av[i] * bv[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int gr = row0 + lr + R * i;
+        if (gr >= m) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int gc = col0 + lc + C * j;
+            if (gc < n) c[static_cast<std::ptrdiff_t>(gr) * n + gc] = acc[i][j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------- FP32 MFMA
+//
+// Block tile 128x128, K step 32, 256 lanes = 4 waves in a 2x2 grid, each wave
+// a 64x64 quadrant as 2x2 v_mfma_f32_32x32x2_f32 accumulators (64 VGPRs).
+//
+// LDS: A row-major (k contiguous, row pitch 36 floats), B row-major (n
+// contiguous, pitch 132). With 36-float rows, eight lanes reading 16 bytes
+// each from eight consecutive rows touch 32 distinct banks.
+//
+// MFMA operand order. One v_mfma_f32_32x32x2_f32 multiplies a 32x2 slice of A
+// by a 2x32 slice of B: lane l supplies row/column l % 32 and k slot l / 32.
+// The result does not depend on which K index each (step, slot) pair stands
+// for, as long as A and B use the same pairing; step s, slot h here stands
+// for k = 16h + s of the 32-wide tile, so a lane reads its A values as four
+// 16-byte vectors.
+//
+// Accumulator layout (32x32 result, 16 floats per lane): value v of lane l is
+// row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.
+
+constexpr int kMBM = 128, kMBN = 128, kMBK = 32;
+constexpr int kAPitch = kMBK + 4;
+constexpr int kBPitch = kMBN + 4;
+
+// 4 consecutive floats of a row-major matrix (leading dimension ld) from
+// (row, col); zeros at or past row_end / col_end. kVec: one 16-byte load
+// (rows 16-byte aligned and col_end a multiple of 4).
+template <bool kVec>
+__device__ __forceinline__ f32x4 load4(const float* __restrict__ p, int row, int col, int row_end, int col_end,
+                                       int ld) {
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row >= row_end) return v;
+    const float* s = p + static_cast<std::ptrdiff_t>(row) * ld + col;
+    if constexpr (kVec) {
+        if (col < col_end) v = *reinterpret_cast<const f32x4*>(s);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (col + e < col_end) v[e] = s[e];
+        }
+    }
+    return v;
+}
+
+template <bool kDouble, bool kVec>
+__global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ c, int m, int n, int k, int k_split,
+                                                          float* __restrict__ partial) {
+    constexpr int S = kDouble ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) float as[S][kMBM][kAPitch];
+    __shared__ __attribute__((aligned(16))) float bs[S][kMBK][kBPitch];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64;
+    const int wr = (wave / 2) * 64, wc = (wave % 2) * 64;
+    const int half = lane / 32, li = lane % 32;
+    const int row0 = blockIdx.y * kMBM, col0 = blockIdx.x * kMBN;
+    const int kb = blockIdx.z * k_split;
+    const int ke = min(k, kb + k_split);
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    // Per tile: A is 128 rows x 8 vectors, B 32 rows x 32 vectors; 4 of each per lane.
+    f32x4 ra[4], rb[4];
+    auto global_load = [&](int k0) {
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int f = tid + l * 256;
+            ra[l] = load4<kVec>(a, row0 + f / 8, k0 + (f % 8) * 4, m, ke, k);
+            rb[l] = load4<kVec>(b, k0 + f / 32, col0 + (f % 32) * 4, ke, n, n);
+        }
+    };
+    auto lds_store = [&](int s) {
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int f = tid + l * 256;
+            *reinterpret_cast<f32x4*>(&as[s][f / 8][(f % 8) * 4]) = ra[l];
+            *reinterpret_cast<f32x4*>(&bs[s][f / 32][(f % 32) * 4]) = rb[l];
+        }
+    };
+    auto multiply = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < kMBK / 8; ++q) {
+            f32x4 av[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) av[i] = *reinterpret_cast<const f32x4*>(&as[s][wr + i * 32 + li][half * 16 + q * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int kk = half * 16 + q * 4 + e;
+                float bv[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) bv[j] = bs[s][kk][wc + j * 32 + li];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    const int tiles = ke > kb ? (ke - kb + kMBK - 1) / kMBK : 0;
+    if constexpr (kDouble) {
+        if (tiles > 0) {
+            global_load(kb);
+            lds_store(0);
+        }
+        __syncthreads();
+        for (int t = 0; t < tiles; ++t) {
+            const int cur = t & 1;
+            const bool more = t + 1 < tiles;
+            if (more) global_load(kb + (t + 1) * kMBK);
+            multiply(cur);
+            // The other stage was last read before the previous barrier.
+            if (more) lds_store(cur ^ 1);
+            __syncthreads();
+        }
+    } else {
+        for (int t = 0; t < tiles; ++t) {
+            global_load(kb + t * kMBK);
+            __syncthreads();  // every wave is done with the previous tile
+            lds_store(0);
+            __syncthreads();
+            multiply(0);
+        }
+    }
+
+    float* __restrict__ out = gridDim.z == 1 ? c : partial + static_cast<std::ptrdiff_t>(blockIdx.z) * m * n;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = col0 + wc + j * 32 + li;
+            if (col >= n) continue;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = row0 + wr + i * 32 + 8 * (v / 4) + 4 * half + (v % 4);
+                if (row < m) out[static_cast<std::ptrdiff_t>(row) * n + col] = acc[i][j][v];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- split-K sum
+
+__global__ void __launch_bounds__(256) sum_splits(const float* __restrict__ partial, float* __restrict__ c,
+                                                  std::size_t count, int splits) {
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * 256;
+    for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x; i < count; i += stride) {
+        float s = partial[i];
+        for (int z = 1; z < splits; ++z) s += partial[static_cast<std::size_t>(z) * count + i];
+        c[i] = s;
+    }
+}
+
+__global__ void __launch_bounds__(256) sum_splits_vec(const f32x4* __restrict__ partial, f32x4* __restrict__ c,
+                                                      std::size_t count4, int splits) {
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * 256;
+    for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x; i < count4; i += stride) {
+        f32x4 s = partial[i];
+        for (int z = 1; z < splits; ++z) s += partial[static_cast<std::size_t>(z) * count4 + i];
+        c[i] = s;
+    }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16 == 0; }
+
+int split_len(int k, int splits, int step) {
+    if (splits <= 1) return std::max(k, 1);
+    const int per = (k + splits - 1) / splits;
+    return (per + step - 1) / step * step;
+}
+
+int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
+                    hipStream_t stream, int splits, float* workspace) {
+    const int k_split = split_len(k, splits, kMBK);
+    const int depth = std::max(1, (k + k_split - 1) / k_split);
+    if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((n + kMBN - 1) / kMBN, (m + kMBM - 1) / kMBM, depth);
+    const bool vec = n % 4 == 0 && k % 4 == 0 && aligned16(a) && aligned16(b);
+    float* out_ws = depth > 1 ? workspace : nullptr;
+    if (double_buffer) {
+        if (vec) {
+            hipLaunchKernelGGL((matmul_mfma_f32<true, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
+        } else {
+            hipLaunchKernelGGL((matmul_mfma_f32<true, false>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
+        }
+    } else {
+        if (vec) {
+            hipLaunchKernelGGL((matmul_mfma_f32<false, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
+        } else {
+            hipLaunchKernelGGL((matmul_mfma_f32<false, false>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
+        }
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || depth == 1) return e;
+    return mchip_sum_split_partials(workspace, c, static_cast<std::size_t>(m) * n, depth, stream);
+}
+
+}  // namespace
+
+extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = count % 4 == 0 && aligned16(partial) && aligned16(c);
+    const std::size_t items = vec ? count / 4 : count;
+    const unsigned blocks = static_cast<unsigned>(std::max<std::size_t>(1, std::min<std::size_t>((items + 255) / 256, 8192)));
+    if (vec) {
+        hipLaunchKernelGGL(sum_splits_vec, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const f32x4*>(partial),
+                           reinterpret_cast<f32x4*>(c), items, splits);
+    } else {
+        hipLaunchKernelGGL(sum_splits, dim3(blocks), dim3(256), 0, s, partial, c, items, splits);
+    }
+    return hipGetLastError();
+}
+
+extern "C" int mchip_launch_tensor_core(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                        void* stream, int splits, float* workspace);
+
+extern "C" int mchip_launch_matmul(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                   void* stream, int splits, float* workspace) {
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (kernel) {
+        case kNaive: {
+            const dim3 grid((n + 15) / 16, (m + 15) / 16);
+            hipLaunchKernelGGL(matmul_naive, grid, dim3(16, 16), 0, s, a, b, c, m, n, k);
+            return hipGetLastError();
+        }
+        case kTiled: {
+            const dim3 grid((n + kTile - 1) / kTile, (m + kTile - 1) / kTile);
+            hipLaunchKernelGGL(matmul_tiled, grid, dim3(kTile, kTile), 0, s, a, b, c, m, n, k);
+            return hipGetLastError();
+        }
+        case kRegisterTiled128: {
+            const dim3 grid((n + 127) / 128, (m + 127) / 128);
+            hipLaunchKernelGGL((matmul_register_tiled<128, 128, 8, 8, 8>), grid, dim3(256), 0, s, a, b, c, m, n, k);
+            return hipGetLastError();
+        }
+        case kRegisterTiled64: {
+            const dim3 grid((n + 63) / 64, (m + 63) / 64);
+            hipLaunchKernelGGL((matmul_register_tiled<64, 64, 8, 4, 4>), grid, dim3(256), 0, s, a, b, c, m, n, k);
+            return hipGetLastError();
+        }
+        case kVectorized: return launch_mfma_f32(false, a, b, c, m, n, k, s, 1, nullptr);
+        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr);
+        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace);
+        case kTensorCoreTf32:
+        case kTensorCoreBf16:
+        case kTensorCoreF16: return mchip_launch_tensor_core(kernel, a, b, c, m, n, k, stream, splits, workspace);
+        default: return hipErrorInvalidValue;  // Auto must be resolved first
+    }
+}

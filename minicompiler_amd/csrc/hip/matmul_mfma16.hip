@@ -1,0 +1,292 @@
+// bf16 / fp16 matrix-core matmul for gfx950 (v_mfma_f32_16x16x32_bf16 and
+// _f16), FP32 accumulation and output. Takes the place of the reference's
+// tensor-core kernels (src/cuda/matmul_tensor_core.cu:96-297):
+//   - fp32 inputs rounded to nearest-even into bf16 / fp16 as they are
+//     staged into LDS (the reference's mode), or
+//   - inputs already in bf16 / fp16 in device memory (the pre-cast mode).
+// TF32 does not exist on gfx950 (no xf32 matrix instruction): those requests
+// report hipErrorNotSupported.
+//
+// Block tile 128x128, K step 64, 256 lanes = 4 waves in a 2x2 grid, each wave
+// a 64x64 quadrant as 4x4 16x16 accumulators. A is staged row-major
+// (k contiguous), B transposed (n-major, k contiguous), so each lane's MFMA
+// operand is one 16-byte LDS read. Two LDS stages; split-K as in the FP32
+// kernels.
+//
+// v_mfma_f32_16x16x32_*: lane l supplies row (A) / column (B) l % 16 and
+// eight k values from group l / 16; A and B use the same k assignment, so
+// any assignment gives the same sum (here group g holds k = 8g .. 8g+7 of the
+// 32-wide step). Result: value v of lane l is row 4 (l / 16) + v, column l % 16.
+
+#include "matmul.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum { kTensorCoreTf32 = 8, kTensorCoreBf16 = 9, kTensorCoreF16 = 10 };
+
+// Round-to-nearest-even of a float to the upper 16 bits (bf16). NaN stays a
+// quiet NaN; values that round past the largest finite bf16 become infinity.
+__device__ __forceinline__ unsigned short to_bf16_bits(float x) {
+    const unsigned u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x0040u);
+    const unsigned rounded = u + 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<unsigned short>(rounded >> 16);
+}
+
+// IEEE half, round to nearest even (the hardware conversion).
+__device__ __forceinline__ unsigned short to_f16_bits(float x) {
+    const _Float16 h = static_cast<_Float16>(x);
+    return __builtin_bit_cast(unsigned short, h);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ unsigned short to_bits(float x) {
+    if constexpr (kBf16) return to_bf16_bits(x);
+    return to_f16_bits(x);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ f32x4 mfma(u16x8 a, u16x8 b, f32x4 c) {
+    if constexpr (kBf16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+}
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kPitch = kBK + 8;  // halves per LDS row: 144 bytes, keeps 16-byte alignment
+
+// Element source: fp32 in memory (rounded here) or 16-bit already.
+template <bool kBf16, bool kF32In>
+struct Source {
+    using T = typename std::conditional<kF32In, float, unsigned short>::type;
+};
+
+// Four consecutive elements as 16-bit patterns; zeros out of range.
+template <bool kBf16, bool kF32In, bool kVec>
+__device__ __forceinline__ u16x4 load4(const void* __restrict__ base, int row, int col, int row_end, int col_end,
+                                       int ld) {
+    u16x4 v = {0, 0, 0, 0};
+    if (row >= row_end) return v;
+    if constexpr (kF32In) {
+        const float* s = static_cast<const float*>(base) + static_cast<std::ptrdiff_t>(row) * ld + col;
+        if constexpr (kVec) {
+            if (col < col_end) {
+                const f32x4 f = *reinterpret_cast<const f32x4*>(s);
+                v = u16x4{to_bits<kBf16>(f.x), to_bits<kBf16>(f.y), to_bits<kBf16>(f.z), to_bits<kBf16>(f.w)};
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (col + e < col_end) v[e] = to_bits<kBf16>(s[e]);
+            }
+        }
+    } else {
+        const unsigned short* s =
+            static_cast<const unsigned short*>(base) + static_cast<std::ptrdiff_t>(row) * ld + col;
+        if constexpr (kVec) {
+            if (col < col_end) v = *reinterpret_cast<const u16x4*>(s);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (col + e < col_end) v[e] = s[e];
+            }
+        }
+    }
+    return v;
+}
+
+template <bool kBf16, bool kF32In, bool kVec>
+__global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__ a, const void* __restrict__ b,
+                                                        float* __restrict__ c, int m, int n, int k, int k_split,
+                                                        float* __restrict__ partial) {
+    __shared__ __attribute__((aligned(16))) unsigned short as[2][kBM][kPitch];
+    __shared__ __attribute__((aligned(16))) unsigned short bt[2][kBN][kPitch];
+
+    const int tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64;
+    const int wr = (wave / 2) * 64, wc = (wave % 2) * 64;
+    const int g = lane / 16, li = lane % 16;
+    const int row0 = blockIdx.y * kBM, col0 = blockIdx.x * kBN;
+    const int kb = blockIdx.z * k_split;
+    const int ke = min(k, kb + k_split);
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // A tile: 128 rows x 16 quads; B tile: 64 rows x 32 quads. 8 of each per lane.
+    u16x4 ra[8], rb[8];
+    auto global_load = [&](int k0) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int f = tid + l * 256;
+            ra[l] = load4<kBf16, kF32In, kVec>(a, row0 + f / 16, k0 + (f % 16) * 4, m, ke, k);
+            rb[l] = load4<kBf16, kF32In, kVec>(b, k0 + f / 32, col0 + (f % 32) * 4, ke, n, n);
+        }
+    };
+    auto lds_store = [&](int s) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const int f = tid + l * 256;
+            *reinterpret_cast<u16x4*>(&as[s][f / 16][(f % 16) * 4]) = ra[l];
+            const int kk = f / 32, cc = (f % 32) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bt[s][cc + e][kk] = rb[l][e];
+        }
+    };
+    auto multiply = [&](int s) {
+#pragma unroll
+        for (int q = 0; q < kBK / 32; ++q) {
+            u16x8 av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const u16x8*>(&as[s][wr + i * 16 + li][q * 32 + g * 8]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = *reinterpret_cast<const u16x8*>(&bt[s][wc + j * 16 + li][q * 32 + g * 8]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma<kBf16>(av[i], bv[j], acc[i][j]);
+        }
+    };
+
+    const int tiles = ke > kb ? (ke - kb + kBK - 1) / kBK : 0;
+    if (tiles > 0) {
+        global_load(kb);
+        lds_store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < tiles; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < tiles;
+        if (more) global_load(kb + (t + 1) * kBK);
+        multiply(cur);
+        if (more) lds_store(cur ^ 1);
+        __syncthreads();
+    }
+
+    float* __restrict__ out = gridDim.z == 1 ? c : partial + static_cast<std::ptrdiff_t>(blockIdx.z) * m * n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = col0 + wc + j * 16 + li;
+            if (col >= n) continue;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = row0 + wr + i * 16 + 4 * g + v;
+                if (row < m) out[static_cast<std::ptrdiff_t>(row) * n + col] = acc[i][j][v];
+            }
+        }
+    }
+}
+
+bool aligned(const void* p, std::uintptr_t bytes) { return reinterpret_cast<std::uintptr_t>(p) % bytes == 0; }
+
+int split_len(int k, int splits, int step) {
+    if (splits <= 1) return std::max(k, 1);
+    const int per = (k + splits - 1) / splits;
+    return (per + step - 1) / step * step;
+}
+
+template <bool kBf16, bool kF32In>
+int launch16(const void* a, const void* b, float* c, int m, int n, int k, hipStream_t stream, int splits,
+             float* workspace) {
+    const int k_split = split_len(k, splits, kBK);
+    const int depth = std::max(1, (k + k_split - 1) / k_split);
+    if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM, depth);
+    const std::uintptr_t align = kF32In ? 16 : 8;
+    const bool vec = n % 4 == 0 && k % 4 == 0 && aligned(a, align) && aligned(b, align);
+    float* ws = depth > 1 ? workspace : nullptr;
+    if (vec) {
+        hipLaunchKernelGGL((matmul_mfma16<kBf16, kF32In, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, ws);
+    } else {
+        hipLaunchKernelGGL((matmul_mfma16<kBf16, kF32In, false>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, ws);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || depth == 1) return e;
+    return mchip_sum_split_partials(workspace, c, static_cast<std::size_t>(m) * n, depth, stream);
+}
+
+__global__ void __launch_bounds__(256) convert_kernel(const float* __restrict__ in, unsigned short* __restrict__ out,
+                                                      std::size_t count, int bf16) {
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * 256;
+    for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x; i < count; i += stride) {
+        out[i] = bf16 ? to_bf16_bits(in[i]) : to_f16_bits(in[i]);
+    }
+}
+
+}  // namespace
+
+extern "C" int mchip_launch_tensor_core(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                        void* stream, int splits, float* workspace) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    switch (kernel) {
+        case kTensorCoreBf16: return launch16<true, true>(a, b, c, m, n, k, s, splits, workspace);
+        case kTensorCoreF16: return launch16<false, true>(a, b, c, m, n, k, s, splits, workspace);
+        case kTensorCoreTf32: return hipErrorNotSupported;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+extern "C" int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n,
+                                        int k, void* stream, int splits, float* workspace) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    if (kernel == kTensorCoreTf32) return hipErrorNotSupported;
+    if (kernel == kTensorCoreBf16 && dtype == MCHIP_DTYPE_BF16) {
+        return launch16<true, false>(a, b, c, m, n, k, s, splits, workspace);
+    }
+    if (kernel == kTensorCoreF16 && dtype == MCHIP_DTYPE_F16) {
+        return launch16<false, false>(a, b, c, m, n, k, s, splits, workspace);
+    }
+    return hipErrorInvalidValue;
+}
+
+extern "C" int mchip_matmul_supported(int kernel) { return kernel != kTensorCoreTf32; }
+
+extern "C" int mchip_matmul_blocks_per_cu(int kernel) {
+    int blocks = 0;
+    hipError_t e = hipErrorInvalidValue;
+    switch (kernel) {
+        case kTensorCoreBf16:
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, matmul_mfma16<true, true, true>, 256, 0);
+            break;
+        case kTensorCoreF16:
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, matmul_mfma16<false, true, true>, 256, 0);
+            break;
+        default: return 2;
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return 1;
+    }
+    return std::max(blocks, 1);
+}
+
+extern "C" int mchip_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream) {
+    if (dtype != MCHIP_DTYPE_BF16 && dtype != MCHIP_DTYPE_F16) return hipErrorInvalidValue;
+    const unsigned blocks = static_cast<unsigned>(std::max<std::size_t>(1, std::min<std::size_t>((count + 255) / 256, 8192)));
+    hipLaunchKernelGGL(convert_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), in,
+                       static_cast<unsigned short*>(out), count, dtype == MCHIP_DTYPE_BF16 ? 1 : 0);
+    return hipGetLastError();
+}

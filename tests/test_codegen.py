@@ -1,0 +1,128 @@
+"""The elementwise kernel generator, without a GPU: the reference's generator
+known answers (tests/test_cuda_codegen.cpp:29-109) restated for the HIP
+text, and hipRTC compiling the generated kernels for gfx950 offline."""
+
+import re
+
+import pytest
+
+GELU = """input x : f32[8, 64]
+const coef : f32[] = 0.044715
+const c : f32[] = 0.7978846
+const half : f32[] = 0.5
+const one : f32[] = 1.0
+x2 = mul x, x
+x3 = mul x2, x
+t = mul x3, coef
+inner = add x, t
+u = mul inner, c
+th = tanh u
+hx = mul x, half
+p = add th, one
+y = mul hx, p
+output y
+"""
+
+
+def kernel_loop(src):
+    return src.index("for (; i +")
+
+
+def test_fused_gelu_is_one_vectorised_kernel(mc):
+    c = mc.Compiled(GELU, passes="fuse", backend="none")
+    (src,) = c.kernel_sources
+    assert "mc_elementwise(float* __restrict__ out, const float* __restrict__ in0, unsigned n)" in src
+    assert "16-byte vector accesses" in src
+    assert "reinterpret_cast<const mc_f32x4*>(in0)[p]" in src
+    # Exact bit patterns, once, in the program (before the kernel's loop).
+    assert src.count("__uint_as_float(0x3f000000u)") == 1
+    assert src.index("0x3f000000u") < kernel_loop(src)
+    assert src.count("tanhf(") == 1               # once in the program ...
+    assert src.count("mc_program(a0[u].") == 8     # ... applied to 4 lanes, full and ragged steps
+
+
+def test_reads_a_bias_row_periodically(mc):
+    add = "r0 = load in0\nr1 = load in1\nr2 = add r0, r1\n"
+    src, vec = mc.generate_elementwise_kernel(add, [(16, 64), (64,)], (16, 64))
+    assert vec and "[(p) % 16u]" in src
+    src, vec = mc.generate_elementwise_kernel(add, [(16, 64), (64,)], (16, 64), allow_vectorize=False)
+    assert not vec and "in1[(p) % 64u]" in src
+    # A period that is not a multiple of 4 would let a vector straddle two repetitions.
+    src, vec = mc.generate_elementwise_kernel(add, [(16, 6), (6,)], (16, 6))
+    assert not vec and "in1[(p) % 6u]" in src
+
+
+def test_general_broadcasts_use_constant_index_math(mc):
+    mul = "r0 = load in0\nr1 = load in1\nr2 = mul r0, r1\n"
+    src, vec = mc.generate_elementwise_kernel(mul, [(5, 4, 6), (5, 1, 6)], (5, 4, 6))
+    assert not vec
+    assert "in0[p]" in src
+    assert "return (i / 24u) * 6u + (i % 6u);" in src and "in1[mc_general_1(p)]" in src
+    src, _ = mc.generate_elementwise_kernel(mul, [(7, 9), (7, 1)], (7, 9))
+    assert "return (i / 9u);" in src
+
+
+def test_scalar_inputs_are_loaded_once_before_the_loop(mc):
+    div = "r0 = load in0\nr1 = load in1\nr2 = div r0, r1\n"
+    src, vec = mc.generate_elementwise_kernel(div, [(1000,), ()], (1000,))
+    assert "const float s1 = in1[0];" in src and src.index("const float s1 = in1[0];") < kernel_loop(src)
+    assert "const float r2 = r0 / r1;" in src
+    assert vec  # 1000 is a multiple of 4
+    _, vec = mc.generate_elementwise_kernel(div, [(1001,), ()], (1001,))
+    assert not vec
+
+
+def test_immediates_are_exact_bit_patterns(mc):
+    prog = "r0 = load in0\nr1 = imm 0xbdcccccd\nr2 = mul r0, r1\nr3 = imm 0x7f800000\nr4 = add r2, r3\n"
+    src, _ = mc.generate_elementwise_kernel(prog, [(8,)], (8,))
+    assert "__uint_as_float(0xbdcccccdu)" in src  # -0.1f
+    assert "__uint_as_float(0x7f800000u)" in src  # +inf
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = imm -0.1\nr2 = mul r0, r1\n", [(8,)], (8,))
+    assert "__uint_as_float(0xbdcccccdu)" in src
+
+
+UNARY = ["neg", "exp", "log", "sqrt", "relu", "sigmoid", "tanh"]
+BINARY = ["add", "sub", "mul", "div"]
+
+
+def test_every_op_is_emitted(mc):
+    for op in UNARY:
+        src, _ = mc.generate_elementwise_kernel(f"r0 = load in0\nr1 = {op} r0\n", [(4,)], (4,))
+        assert "not an elementwise op" not in src
+    for op in BINARY:
+        src, _ = mc.generate_elementwise_kernel(f"r0 = load in0\nr1 = load in1\nr2 = {op} r0, r1\n", [(4,), (4,)], (4,))
+        assert "not an elementwise op" not in src
+
+
+def test_items_per_lane_controls_the_unroll(mc):
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = neg r0\n", [(4096,)], (4096,), items_per_lane=2)
+    assert "for (; i + 256u < n; i += step)" in src and "gridDim.x * 512u" in src
+
+
+def test_rejects_malformed_programs(mc):
+    with pytest.raises(mc.MinicompilerError):
+        mc.generate_elementwise_kernel("r0 = load in3\n", [(4,)], (4,))
+    with pytest.raises(mc.MinicompilerError):
+        mc.generate_elementwise_kernel("r0 = load in0\nr1 = add r0, r5\n", [(4,)], (4,))
+
+
+@pytest.mark.parametrize("text,shapes,out", [
+    (GELU, None, None),
+    ("r0 = load in0\nr1 = load in1\nr2 = sub r0, r1\nr3 = load in2\nr4 = div r2, r3\nr5 = relu r4\n",
+     [(64, 256), (256,), (256,)], (64, 256)),
+    ("r0 = load in0\nr1 = load in1\nr2 = mul r0, r1\nr3 = sigmoid r2\nr4 = log r3\nr5 = exp r4\nr6 = sqrt r5\n",
+     [(5, 4, 6), (5, 1, 6)], (5, 4, 6)),
+    ("r0 = load in0\nr1 = load in1\nr2 = add r0, r1\n", [(17, 1), (1, 33)], (17, 33)),
+])
+def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, out):
+    if shapes is None:
+        src = mc.Compiled(text, passes="fuse", backend="none").kernel_sources[0]
+    else:
+        src, _ = mc.generate_elementwise_kernel(text, shapes, out)
+    ok, log = mc.compile_kernel_source(src, "gfx950")
+    assert ok, log
+
+
+def test_a_bad_generated_source_returns_the_hiprtc_log(mc):
+    ok, log = mc.compile_kernel_source('extern "C" __global__ void mc_elementwise() { undefined_thing(); }')
+    assert not ok and "undefined_thing" in log and "hipRTC could not compile" in log

@@ -14,8 +14,9 @@
  * 1 on failure and record a message readable with mc_last_error() (per
  * thread). Device-level calls (mc_launch_*, mc_device_*, mc_memcpy_*, ...)
  * return the hipError_t value; mc_error_string() describes it. Text-out
- * calls write at most `size` bytes including the terminating NUL and return
- * the full length of the text (like snprintf), or -1 on failure.
+ * calls of part 2 write at most `size` bytes including the terminating NUL
+ * and return the full length of the text (like snprintf), or -1 on failure;
+ * those of part 1 keep the reference's return codes.
  * Handles are not thread-safe; one handle, one thread at a time. */
 #ifndef MINICOMPILER_HIP_H
 #define MINICOMPILER_HIP_H
@@ -55,7 +56,8 @@ MC_API int mc_enqueue(void* handle, void* stream);
 MC_API int mc_download(void* handle, float* const* outputs);
 /* Kernel launches per mc_enqueue, -1 without an executable. (capi.cpp:174-182) */
 MC_API int mc_kernel_launches(void* handle);
-/* The matmul kernel of each matmul, comma-separated. (capi.cpp:186-202) */
+/* The matmul kernel of each matmul, comma-separated, truncated to `size`.
+ * Returns 0, or 1 without an executable (not a length: capi.cpp:184-202). */
 MC_API int mc_matmul_kernels(void* handle, char* out, int size);
 /* Engine clock in MHz as the runtime reports it, 0 without a device. (capi.cpp:204-210) */
 MC_API double mc_gpu_sm_clock_mhz(void);

@@ -422,8 +422,11 @@ class Compiled:
 
     @property
     def matmul_kernels(self) -> list[str]:
-        text = _text_call(library().mc_matmul_kernels, self._h)
-        return [s for s in text.split(",") if s]
+        # Returns 0 or 1 like the reference's (bench/capi.cpp:184-202), not a length.
+        buf = ctypes.create_string_buffer(64 * max(1, self.kernel_launches) + 64)
+        if library().mc_matmul_kernels(self._h, buf, len(buf)) != 0:
+            raise MinicompilerError(last_error())
+        return [s for s in buf.value.decode().split(",") if s]
 
     @property
     def kernel_sources(self) -> list[str]:

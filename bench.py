@@ -229,12 +229,25 @@ def cpu_baseline(batch_rows: int, seconds: float) -> dict:
                       f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM), 1 thread, {os.cpu_count()} host cores"}
 
 
+def measured_traffic(workload: str, launch: str):
+    """HBM bytes per launch of `launch` in `workload`, from the rocprofv3
+    FETCH_SIZE and WRITE_SIZE runs summarised in profiles/traffic.json (each
+    counter scaled by what it reads for the copy_neg calibration kernel of
+    known size), or None when that kernel has not been counted."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("kernels", {}).get(f"{workload} | {launch}")
+    return None if entry is None else entry["traffic_bytes"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="mlp", choices=["mlp", "gelu", "batchnorm", "gemm_fp32", "gemm_bf16"])
+    ap.add_argument("--workload", default="mlp",
+                    choices=["mlp", "gelu", "batchnorm", "gemm_fp32", "gemm_bf16", "copy"])
     ap.add_argument("--batch", type=int, default=8192)
     ap.add_argument("--quick", action="store_true", help="headline workload only (no other configs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -274,6 +287,14 @@ def main() -> int:
     else:
         line["unit"] = "GB/s" if args.workload in ("gelu", "batchnorm") else "TFLOP/s"
 
+    if args.workload == "copy":
+        # Byte-counter calibration: reads and writes 128 MiB each, known exactly.
+        k = bench_elementwise_graph(mc, "copy_neg", {"M": 8192, "N": 4096}, lambda n: mc.uniform(n, 1, -1.0, 1.0),
+                                    args.steps, args.warmup)
+        line.update({"value": k["gbs"], "ms_per_step": k["ms_per_step"], "dtype": "f32",
+                     "config": {"workload": "copy_neg (counter calibration)", **k["dims"]},
+                     "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
+                                  "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
     if args.workload in ("gelu", "batchnorm") or (args.workload == "mlp" and not args.quick):
         cfgs = line.setdefault("configs", {})
         if args.workload != "batchnorm":
@@ -311,6 +332,8 @@ def main() -> int:
                          "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
                                       "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
 
+    if "roofline" in line:
+        line["roofline"]["traffic"] = measured_traffic(line["config"]["workload"], line["roofline"]["kernel"])
     line["device"] = {k: dev[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
     if not args.no_cpu_baseline and args.workload == "mlp":
         line["cpu_baseline"] = cpu_baseline(256, args.cpu_seconds)

@@ -198,6 +198,215 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
     }
 }
 
+// ---------------------------------------------------------------- fast path
+//
+// 16-bit inputs already in HBM, K a multiple of 64, rows 16-byte aligned.
+// Block tile 256x256x64, 256 lanes = 4 waves in a 2x2 grid, each wave a
+// 128x128 quadrant as 8x8 accumulators of v_mfma_f32_16x16x32 (256 fp32 per
+// lane). One block per CU: two LDS stages of 64 KiB.
+//
+// Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
+// 16 bytes at (LDS base + 16 l), so one wave instruction fills 1 KiB of
+// LDS; the swizzles below are applied by choosing which global chunk each
+// lane fetches. Rows and columns past the matrix edge are clamped to the
+// last row / column chunk, so every fetch is in bounds; the values they
+// bring only reach C rows or columns that are not stored.
+//
+// LDS layout of a stage (bytes):
+//   A [256 rows][8 chunks of 8 k]: row r at 128 r; logical chunk c stored at
+//     chunk c ^ fa(r), fa(r) = (r ^ (r >> 3)) & 7. The ds_read_b128 of a
+//     fragment (16 rows, one chunk) then touches distinct banks whether the
+//     LDS serves 8 or 16 such lanes per cycle.
+//   B [64 k rows][32 chunks of 8 n], at +32 KiB: k row kr at 512 kr; logical
+//     chunk c stored at chunk c ^ 2 tb(kr), tb(kr) = (kr & 3) | ((kr >> 3) & 3) << 2,
+//     i.e. 32-byte pairs XOR tb. B stays n-contiguous and is read with
+//     ds_read_b64_tr_b16: within each 16 lanes, lane 4e + c supplies the
+//     address of 4 values (row e, columns 4c..4c+3) and lane i receives
+//     column i of rows 0..3. Two such reads give a lane the 8 consecutive k
+//     of one column that the MFMA B operand needs. The 16 rows one read
+//     instruction touches fall in distinct 32-byte bank windows.
+//
+// The MFMA is issued with the B fragment as its first operand and the A
+// fragment as its second, which yields C^T tiles: value v of lane l is
+// C[m0 + l % 16][n0 + 4 (l / 16) + v], four consecutive columns, stored as
+// one 16-byte write.
+//
+// Tiles are handed out XCD by XCD (block b runs on XCD b % 8): each XCD gets
+// a contiguous run of tiles, ordered in groups of 8 tile rows, so the blocks
+// resident on one XCD share A and B panels in its L2.
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define MC_LDS __attribute__((address_space(3)))
+
+constexpr int kFBM = 256, kFBN = 256, kFBK = 64;
+constexpr int kFStage = 64 * 1024;
+constexpr int kFBOffset = 32 * 1024;
+constexpr int kFGroupM = 8;
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz_b(int kr) { return (kr & 3) | (((kr >> 3) & 3) << 2); }
+
+template <bool kBf16>
+__global__ void __launch_bounds__(256, 1) matmul_mfma16_fast(const unsigned short* __restrict__ a,
+                                                             const unsigned short* __restrict__ b,
+                                                             float* __restrict__ c, int m, int n, int k) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kFStage];
+    MC_LDS unsigned char* lds = (MC_LDS unsigned char*)(smem);  // generic -> LDS address space
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+
+    // Tile of this block.
+    const int tiles_m = (m + kFBM - 1) / kFBM, tiles_n = (n + kFBN - 1) / kFBN;
+    const int blocks = static_cast<int>(gridDim.x);
+    int id = static_cast<int>(blockIdx.x);
+    if (blocks % kXcds == 0) id = (id % kXcds) * (blocks / kXcds) + id / kXcds;
+    const int per_group = kFGroupM * tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * kFGroupM;
+    const int rows_in_group = min(tiles_m - first_m, kFGroupM);
+    const int in_group = id - group * per_group;
+    const int tm = first_m + in_group % rows_in_group;
+    const int tn = in_group / rows_in_group;
+    const int row0 = tm * kFBM, col0 = tn * kFBN;
+
+    // Global fetch addresses. A: wave w fills rows 64 w .. 64 w + 63, eight
+    // rows per instruction; lane -> (row 64 w + 8 i + l / 8, physical chunk l % 8).
+    const unsigned short* a_src[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = wave * 64 + i * 8 + (lane >> 3);
+        const int lc = (lane & 7) ^ swz_a(r);
+        const int gr = min(row0 + r, m - 1);
+        a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + lc * 8;
+    }
+    // B: wave w fills k rows 16 w .. 16 w + 15, two per instruction; lane ->
+    // (k row 16 w + 2 i + l / 32, physical chunk l % 32).
+    const unsigned short* b_src[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int kr = wave * 16 + i * 2 + (lane >> 5);
+        const int lc = (lane & 31) ^ (2 * swz_b(kr));
+        const int gc = min(col0 + lc * 8, n - 8);
+        b_src[i] = b + static_cast<std::ptrdiff_t>(kr) * n + gc;
+    }
+    const std::ptrdiff_t b_step = static_cast<std::ptrdiff_t>(kFBK) * n;
+
+    auto fetch = [&](int stage, int k0) {
+        MC_LDS unsigned char* sa = lds + stage * kFStage + wave * 64 * 128;
+        MC_LDS unsigned char* sb = lds + stage * kFStage + kFBOffset + wave * 16 * 512;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
+                                             reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[i] + (k0 / kFBK) * b_step),
+                                             reinterpret_cast<MC_LDS void*>(sb + i * 1024), 16, 0, 0);
+        }
+    };
+
+    // LDS read offsets (bytes, within a stage).
+    const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
+    const int li = lane & 15, g = lane >> 4;
+    int a_off[2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int fi = 0; fi < 8; ++fi) {
+            const int r = wr + fi * 16 + li;
+            a_off[q][fi] = r * 128 + (((4 * q + g) ^ swz_a(r)) << 4);
+        }
+    // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
+    // k row 32 q + 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
+    const int te = (lane & 15) >> 2, tc = lane & 3;
+    int b_off[2][2][8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int fj = 0; fj < 8; ++fj) {
+                const int kr = 32 * q + 8 * g + 4 * h + te;
+                const int ncol = wc + fj * 16 + 4 * tc;
+                const int chunk = (ncol >> 3) ^ (2 * swz_b(kr));
+                b_off[q][h][fj] = kFBOffset + kr * 512 + (chunk << 4) + ((ncol & 4) << 1);
+            }
+
+    f32x4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int tiles = k / kFBK;
+    fetch(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int t = 0; t < tiles; ++t) {
+        const int cur = t & 1;
+        if (t + 1 < tiles) fetch(cur ^ 1, (t + 1) * kFBK);
+        MC_LDS unsigned char* st = lds + cur * kFStage;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            u16x8 av[8], bv[8];
+#pragma unroll
+            for (int fi = 0; fi < 8; ++fi) av[fi] = *reinterpret_cast<MC_LDS const u16x8*>(st + a_off[q][fi]);
+#pragma unroll
+            for (int fj = 0; fj < 8; ++fj) {
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    reinterpret_cast<MC_LDS s16x4*>(st + b_off[q][0][fj]));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    reinterpret_cast<MC_LDS s16x4*>(st + b_off[q][1][fj]));
+                bv[fj] = u16x8{static_cast<unsigned short>(lo[0]), static_cast<unsigned short>(lo[1]),
+                               static_cast<unsigned short>(lo[2]), static_cast<unsigned short>(lo[3]),
+                               static_cast<unsigned short>(hi[0]), static_cast<unsigned short>(hi[1]),
+                               static_cast<unsigned short>(hi[2]), static_cast<unsigned short>(hi[3])};
+            }
+#pragma unroll
+            for (int fi = 0; fi < 8; ++fi)
+#pragma unroll
+                for (int fj = 0; fj < 8; ++fj) acc[fi][fj] = mfma<kBf16>(bv[fj], av[fi], acc[fi][fj]);
+        }
+        // The fetch of the next tile has landed and every wave is done with this one.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // acc[fi][fj] holds C[row0 + wr + 16 fi + l % 16][col0 + wc + 16 fj + 4 (l / 16) + v].
+#pragma unroll
+    for (int fi = 0; fi < 8; ++fi) {
+        const int row = row0 + wr + fi * 16 + li;
+        if (row >= m) continue;
+        float* crow = c + static_cast<std::ptrdiff_t>(row) * n;
+#pragma unroll
+        for (int fj = 0; fj < 8; ++fj) {
+            const int col = col0 + wc + fj * 16 + 4 * g;
+            if (col < n) *reinterpret_cast<f32x4*>(crow + col) = acc[fi][fj];
+        }
+    }
+}
+
+// The fast path takes 16-bit A and B with K a multiple of 64, N a multiple
+// of 8 (every 16-byte B chunk wholly inside or outside a row), K and N rows
+// 16-byte aligned, C rows 16-byte aligned, and no split.
+bool fast_eligible(const void* a, const void* b, const float* c, int m, int n, int k, int splits) {
+    const auto al = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16 == 0; };
+    return splits <= 1 && k % kFBK == 0 && n % 8 == 0 && al(a) && al(b) && al(c) && m >= 1 && n >= 8;
+}
+
+template <bool kBf16>
+int launch_fast(const void* a, const void* b, float* c, int m, int n, int k, hipStream_t stream) {
+    const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
+    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
+                       stream, static_cast<const unsigned short*>(a), static_cast<const unsigned short*>(b), c, m, n,
+                       k);
+    return hipGetLastError();
+}
+
 bool aligned(const void* p, std::uintptr_t bytes) { return reinterpret_cast<std::uintptr_t>(p) % bytes == 0; }
 
 int split_len(int k, int splits, int step) {
@@ -253,11 +462,12 @@ extern "C" int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, co
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
     if (kernel == kTensorCoreTf32) return hipErrorNotSupported;
+    const bool fast = fast_eligible(a, b, c, m, n, k, splits);
     if (kernel == kTensorCoreBf16 && dtype == MCHIP_DTYPE_BF16) {
-        return launch16<true, false>(a, b, c, m, n, k, s, splits, workspace);
+        return fast ? launch_fast<true>(a, b, c, m, n, k, s) : launch16<true, false>(a, b, c, m, n, k, s, splits, workspace);
     }
     if (kernel == kTensorCoreF16 && dtype == MCHIP_DTYPE_F16) {
-        return launch16<false, false>(a, b, c, m, n, k, s, splits, workspace);
+        return fast ? launch_fast<false>(a, b, c, m, n, k, s) : launch16<false, false>(a, b, c, m, n, k, s, splits, workspace);
     }
     return hipErrorInvalidValue;
 }

@@ -200,24 +200,31 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 
 // ---------------------------------------------------------------- fast path
 //
-// 16-bit inputs already in HBM, K a multiple of 64, rows 16-byte aligned.
-// Block tile 256x256x64, 256 lanes = 4 waves in a 2x2 grid, each wave a
-// 128x128 quadrant as 8x8 accumulators of v_mfma_f32_16x16x32 (256 fp32 per
-// lane). One block per CU: two LDS stages of 64 KiB.
+// 16-bit inputs already in HBM, K a multiple of 64, N a multiple of 8, rows
+// 16-byte aligned. Block tile 256x256, 512 lanes = 8 waves in a 2x4 grid
+// (two waves per SIMD), each wave a 128x64 quadrant as 8x4 accumulators of
+// v_mfma_f32_16x16x32 (128 fp32 per lane, in AGPRs). One block per CU; the
+// two waves of a SIMD hide each other's LDS and barrier waits.
+//
+// K is walked in steps of 32 through a ring of four 32 KiB LDS stages: the
+// fetch of step t+3 is in flight while step t+1's operands are read from LDS
+// and step t's MFMAs run. A step ends with a wait for this wave's fetch of
+// step t+2 and a plain s_barrier (no memory fence: a fence would also wait
+// for the fetches still in flight).
 //
 // Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
-// 16 bytes at (LDS base + 16 l), so one wave instruction fills 1 KiB of
-// LDS; the swizzles below are applied by choosing which global chunk each
-// lane fetches. Rows and columns past the matrix edge are clamped to the
-// last row / column chunk, so every fetch is in bounds; the values they
-// bring only reach C rows or columns that are not stored.
+// 16 bytes at (LDS base + 16 l), so one wave instruction fills 1 KiB of LDS;
+// the swizzles below are applied by choosing which global chunk each lane
+// fetches. Rows and columns past the matrix edge are clamped to the last row
+// / column chunk, so every fetch is in bounds; the values they bring only
+// reach C rows or columns that are not stored.
 //
 // LDS layout of a stage (bytes):
-//   A [256 rows][8 chunks of 8 k]: row r at 128 r; logical chunk c stored at
-//     chunk c ^ fa(r), fa(r) = (r ^ (r >> 3)) & 7. The ds_read_b128 of a
-//     fragment (16 rows, one chunk) then touches distinct banks whether the
-//     LDS serves 8 or 16 such lanes per cycle.
-//   B [64 k rows][32 chunks of 8 n], at +32 KiB: k row kr at 512 kr; logical
+//   A [256 rows][4 chunks of 8 k], at 0: row r at 64 r; logical chunk c
+//     stored at chunk c ^ fa(r), fa(r) = ((r >> 1) ^ (r >> 3)) & 3. A
+//     fragment read (16 rows, one chunk per lane, ds_read_b128) then touches
+//     distinct banks whether the LDS serves 8 or 16 such lanes per cycle.
+//   B [32 k rows][32 chunks of 8 n], at 16 KiB: k row kr at 512 kr; logical
 //     chunk c stored at chunk c ^ 2 tb(kr), tb(kr) = (kr & 3) | ((kr >> 3) & 3) << 2,
 //     i.e. 32-byte pairs XOR tb. B stays n-contiguous and is read with
 //     ds_read_b64_tr_b16: within each 16 lanes, lane 4e + c supplies the
@@ -238,20 +245,103 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 #define MC_LDS __attribute__((address_space(3)))
 
-constexpr int kFBM = 256, kFBN = 256, kFBK = 64;
-constexpr int kFStage = 64 * 1024;
-constexpr int kFBOffset = 32 * 1024;
+constexpr int kFBM = 256, kFBN = 256, kFBK = 32;
+constexpr int kFThreads = 512;
+constexpr int kFWaves = kFThreads / 64;
+constexpr int kFStages = 4;
+constexpr int kFStage = 32 * 1024;
+constexpr int kFBOffset = 16 * 1024;
 constexpr int kFGroupM = 8;
 constexpr int kXcds = 8;
+constexpr int kFRowFrags = 8;  // 16-row A fragments per wave (128 rows)
+constexpr int kFColFrags = 4;  // 16-column B fragments per wave (64 columns)
+// global_load_lds instructions per wave per step: 2 for A, 2 for B.
+constexpr int kFFetchPerStep = 4;
 
-__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz_a(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 __device__ __forceinline__ int swz_b(int kr) { return (kr & 3) | (((kr >> 3) & 3) << 2); }
 
+// Per-lane addressing, set up once per block.
+struct FastLane {
+    const unsigned short* a_src[2];  // A chunk this lane fetches per instruction (k offset 0)
+    const unsigned short* b_src[2];  // B chunk (k row offset 0)
+    std::ptrdiff_t b_step;           // elements between consecutive K steps of B
+    int a_off[kFRowFrags];           // LDS byte offsets of the A fragments
+    int b_off[2][kFColFrags];        // LDS byte offsets of the two transposed B reads
+    int wave;
+};
+
+__device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastLane& L, int fetch_k) {
+    MC_LDS unsigned char* sa = wr + L.wave * 32 * 64;
+    MC_LDS unsigned char* sb = wr + kFBOffset + L.wave * 4 * 512;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.a_src[i] + fetch_k),
+                                         reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
+    }
+    const std::ptrdiff_t bk = (fetch_k / kFBK) * L.b_step;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.b_src[i] + bk),
+                                         reinterpret_cast<MC_LDS void*>(sb + i * 1024), 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ u16x8 fast_read_a(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
+    return *reinterpret_cast<const MC_LDS u16x8*>(rd + L.a_off[f]);
+}
+
+__device__ __forceinline__ u16x8 fast_read_b(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
+    MC_LDS unsigned char* p = const_cast<MC_LDS unsigned char*>(rd);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[0][f]));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[1][f]));
+    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// One K step: fetch step `fetch_k` into `wr`; multiply the current operands
+// (av, bc) into acc row by row, and as each A fragment is used up read the
+// next step's A fragment into its place; read the next step's B fragments
+// into bn (B fragments stay live for the whole step). `rd` (the next step's
+// stage) and `wr` are distinct stages; declaring them __restrict__ gives the
+// LDS reads alias scopes that keep the compiler from making them wait for
+// the fetch.
 template <bool kBf16>
-__global__ void __launch_bounds__(256, 1) matmul_mfma16_fast(const unsigned short* __restrict__ a,
-                                                             const unsigned short* __restrict__ b,
-                                                             float* __restrict__ c, int m, int n, int k) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kFStage];
+__device__ __forceinline__ void fast_step(const MC_LDS unsigned char* __restrict__ rd, MC_LDS unsigned char* __restrict__ wr,
+                                          const FastLane& L, int fetch_k, u16x8 (&av)[kFRowFrags],
+                                          const u16x8 (&bc)[kFColFrags], u16x8 (&bn)[kFColFrags],
+                                          f32x4 (&acc)[kFRowFrags][kFColFrags]) {
+    fast_fetch(wr, L, fetch_k);
+#pragma unroll
+    for (int fi = 0; fi < kFRowFrags; ++fi) {
+#pragma unroll
+        for (int fj = 0; fj < kFColFrags; ++fj) acc[fi][fj] = mfma<kBf16>(bc[fj], av[fi], acc[fi][fj]);
+        av[fi] = fast_read_a(rd, L, fi);
+        if (fi < kFColFrags) bn[fi] = fast_read_b(rd, L, fi);
+    }
+}
+
+// s_waitcnt with vmcnt = n (n < 16) and expcnt / lgkmcnt left alone.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | n);
+}
+
+// A workgroup barrier without a memory fence; the compiler may not move
+// memory operations or MFMAs across it.
+__device__ __forceinline__ void step_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool kBf16>
+__global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigned short* __restrict__ a,
+                                                                   const unsigned short* __restrict__ b,
+                                                                   float* __restrict__ c, int m, int n, int k) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kFStages * kFStage];
     MC_LDS unsigned char* lds = (MC_LDS unsigned char*)(smem);  // generic -> LDS address space
 
     const int tid = threadIdx.x;
@@ -271,118 +361,92 @@ __global__ void __launch_bounds__(256, 1) matmul_mfma16_fast(const unsigned shor
     const int tn = in_group / rows_in_group;
     const int row0 = tm * kFBM, col0 = tn * kFBN;
 
-    // Global fetch addresses. A: wave w fills rows 64 w .. 64 w + 63, eight
-    // rows per instruction; lane -> (row 64 w + 8 i + l / 8, physical chunk l % 8).
-    const unsigned short* a_src[8];
+    FastLane L;
+    L.wave = wave;
+    // A: wave w fills rows 32 w .. 32 w + 31, sixteen rows per instruction;
+    // lane -> (row 32 w + 16 i + l / 4, physical chunk l % 4).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = wave * 64 + i * 8 + (lane >> 3);
-        const int lc = (lane & 7) ^ swz_a(r);
+    for (int i = 0; i < 2; ++i) {
+        const int r = wave * 32 + i * 16 + (lane >> 2);
+        const int lc = (lane & 3) ^ swz_a(r);
         const int gr = min(row0 + r, m - 1);
-        a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + lc * 8;
+        L.a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + lc * 8;
     }
-    // B: wave w fills k rows 16 w .. 16 w + 15, two per instruction; lane ->
-    // (k row 16 w + 2 i + l / 32, physical chunk l % 32).
-    const unsigned short* b_src[8];
+    // B: wave w fills k rows 4 w .. 4 w + 3, two per instruction; lane ->
+    // (k row 4 w + 2 i + l / 32, physical chunk l % 32).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int kr = wave * 16 + i * 2 + (lane >> 5);
+    for (int i = 0; i < 2; ++i) {
+        const int kr = wave * 4 + i * 2 + (lane >> 5);
         const int lc = (lane & 31) ^ (2 * swz_b(kr));
         const int gc = min(col0 + lc * 8, n - 8);
-        b_src[i] = b + static_cast<std::ptrdiff_t>(kr) * n + gc;
+        L.b_src[i] = b + static_cast<std::ptrdiff_t>(kr) * n + gc;
     }
-    const std::ptrdiff_t b_step = static_cast<std::ptrdiff_t>(kFBK) * n;
-
-    auto fetch = [&](int stage, int k0) {
-        MC_LDS unsigned char* sa = lds + stage * kFStage + wave * 64 * 128;
-        MC_LDS unsigned char* sb = lds + stage * kFStage + kFBOffset + wave * 16 * 512;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(a_src[i] + k0),
-                                             reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_global_load_lds(static_cast<const void*>(b_src[i] + (k0 / kFBK) * b_step),
-                                             reinterpret_cast<MC_LDS void*>(sb + i * 1024), 16, 0, 0);
-        }
-    };
-
-    // LDS read offsets (bytes, within a stage).
-    const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
+    L.b_step = static_cast<std::ptrdiff_t>(kFBK) * n;
+    // Wave (wm, wn) of the 2x4 grid owns rows 128 wm .., columns 64 wn ...
+    const int wr = (wave >> 2) * 128, wc = (wave & 3) * 64;
     const int li = lane & 15, g = lane >> 4;
-    int a_off[2][8];
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int fi = 0; fi < 8; ++fi) {
-            const int r = wr + fi * 16 + li;
-            a_off[q][fi] = r * 128 + (((4 * q + g) ^ swz_a(r)) << 4);
-        }
-    // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
-    // k row 32 q + 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
-    const int te = (lane & 15) >> 2, tc = lane & 3;
-    int b_off[2][2][8];
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int fj = 0; fj < 8; ++fj) {
-                const int kr = 32 * q + 8 * g + 4 * h + te;
-                const int ncol = wc + fj * 16 + 4 * tc;
-                const int chunk = (ncol >> 3) ^ (2 * swz_b(kr));
-                b_off[q][h][fj] = kFBOffset + kr * 512 + (chunk << 4) + ((ncol & 4) << 1);
-            }
-
-    f32x4 acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int tiles = k / kFBK;
-    fetch(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int t = 0; t < tiles; ++t) {
-        const int cur = t & 1;
-        if (t + 1 < tiles) fetch(cur ^ 1, (t + 1) * kFBK);
-        MC_LDS unsigned char* st = lds + cur * kFStage;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            u16x8 av[8], bv[8];
-#pragma unroll
-            for (int fi = 0; fi < 8; ++fi) av[fi] = *reinterpret_cast<MC_LDS const u16x8*>(st + a_off[q][fi]);
-#pragma unroll
-            for (int fj = 0; fj < 8; ++fj) {
-                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    reinterpret_cast<MC_LDS s16x4*>(st + b_off[q][0][fj]));
-                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    reinterpret_cast<MC_LDS s16x4*>(st + b_off[q][1][fj]));
-                bv[fj] = u16x8{static_cast<unsigned short>(lo[0]), static_cast<unsigned short>(lo[1]),
-                               static_cast<unsigned short>(lo[2]), static_cast<unsigned short>(lo[3]),
-                               static_cast<unsigned short>(hi[0]), static_cast<unsigned short>(hi[1]),
-                               static_cast<unsigned short>(hi[2]), static_cast<unsigned short>(hi[3])};
-            }
-#pragma unroll
-            for (int fi = 0; fi < 8; ++fi)
-#pragma unroll
-                for (int fj = 0; fj < 8; ++fj) acc[fi][fj] = mfma<kBf16>(bv[fj], av[fi], acc[fi][fj]);
-        }
-        // The fetch of the next tile has landed and every wave is done with this one.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+    for (int f = 0; f < kFRowFrags; ++f) {
+        const int r = wr + f * 16 + li;
+        L.a_off[f] = r * 64 + ((g ^ swz_a(r)) << 4);
     }
+    // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
+    // k row 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
+    const int te = (lane & 15) >> 2, tc = lane & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int f = 0; f < kFColFrags; ++f) {
+            const int kr = 8 * g + 4 * h + te;
+            const int ncol = wc + f * 16 + 4 * tc;
+            const int chunk = (ncol >> 3) ^ (2 * swz_b(kr));
+            L.b_off[h][f] = kFBOffset + kr * 512 + (chunk << 4) + ((ncol & 4) << 1);
+        }
+
+    f32x4 acc[kFRowFrags][kFColFrags];
+#pragma unroll
+    for (int i = 0; i < kFRowFrags; ++i)
+#pragma unroll
+        for (int j = 0; j < kFColFrags; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int steps = k / kFBK;
+    auto stage = [&](int t) { return lds + (t & (kFStages - 1)) * kFStage; };
+    u16x8 av[kFRowFrags], b0[kFColFrags], b1[kFColFrags];
+    // Prologue: steps 0..2 in flight, then step 0 landed and read.
+    const int pre = min(steps, kFStages - 1);
+    for (int t = 0; t < pre; ++t) fast_fetch(stage(t), L, t * kFBK);
+    __builtin_amdgcn_s_waitcnt(0);
+    step_barrier();
+#pragma unroll
+    for (int f = 0; f < kFRowFrags; ++f) av[f] = fast_read_a(stage(0), L, f);
+#pragma unroll
+    for (int f = 0; f < kFColFrags; ++f) b0[f] = fast_read_b(stage(0), L, f);
+
+    // Steady state, two steps per trip so the B registers alternate without
+    // copies. Every step fetches: past the last step it fetches the last step
+    // again, into the stage of step t-1, which no wave reads any more; every
+    // step reads: past the last step it reads a stage whose values are never
+    // used. So each step ends with this wave's fetches of steps t+2 and t+3
+    // outstanding, and waits for the older one.
+    const int last = (steps - 1) * kFBK;
+    for (int t = 0; t < steps; t += 2) {
+        fast_step<kBf16>(stage(t + 1), stage(t + 3), L, min((t + 3) * kFBK, last), av, b0, b1, acc);
+        wait_vmcnt<kFFetchPerStep>();
+        step_barrier();
+        fast_step<kBf16>(stage(t + 2), stage(t + 4), L, min((t + 4) * kFBK, last), av, b1, b0, acc);
+        wait_vmcnt<kFFetchPerStep>();
+        step_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0);
 
     // acc[fi][fj] holds C[row0 + wr + 16 fi + l % 16][col0 + wc + 16 fj + 4 (l / 16) + v].
 #pragma unroll
-    for (int fi = 0; fi < 8; ++fi) {
+    for (int fi = 0; fi < kFRowFrags; ++fi) {
         const int row = row0 + wr + fi * 16 + li;
         if (row >= m) continue;
         float* crow = c + static_cast<std::ptrdiff_t>(row) * n;
 #pragma unroll
-        for (int fj = 0; fj < 8; ++fj) {
+        for (int fj = 0; fj < kFColFrags; ++fj) {
             const int col = col0 + wc + fj * 16 + 4 * g;
             if (col < n) *reinterpret_cast<f32x4*>(crow + col) = acc[fi][fj];
         }
@@ -390,18 +454,18 @@ __global__ void __launch_bounds__(256, 1) matmul_mfma16_fast(const unsigned shor
 }
 
 // The fast path takes 16-bit A and B with K a multiple of 64, N a multiple
-// of 8 (every 16-byte B chunk wholly inside or outside a row), K and N rows
-// 16-byte aligned, C rows 16-byte aligned, and no split.
+// of 8 (every 16-byte B chunk wholly inside or outside a row), A, B and C
+// 16-byte aligned, and no split.
 bool fast_eligible(const void* a, const void* b, const float* c, int m, int n, int k, int splits) {
     const auto al = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16 == 0; };
-    return splits <= 1 && k % kFBK == 0 && n % 8 == 0 && al(a) && al(b) && al(c) && m >= 1 && n >= 8;
+    return splits <= 1 && k % (2 * kFBK) == 0 && n % 8 == 0 && al(a) && al(b) && al(c) && m >= 1 && n >= 8;
 }
 
 template <bool kBf16>
 int launch_fast(const void* a, const void* b, float* c, int m, int n, int k, hipStream_t stream) {
     const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
     if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
+    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(static_cast<unsigned>(tiles)), dim3(kFThreads), 0,
                        stream, static_cast<const unsigned short*>(a), static_cast<const unsigned short*>(b), c, m, n,
                        k);
     return hipGetLastError();

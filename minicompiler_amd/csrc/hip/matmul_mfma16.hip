@@ -206,11 +206,15 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 // v_mfma_f32_16x16x32 (128 fp32 per lane, in AGPRs). One block per CU; the
 // two waves of a SIMD hide each other's LDS and barrier waits.
 //
-// K is walked in steps of 32 through a ring of four 32 KiB LDS stages: the
-// fetch of step t+3 is in flight while step t+1's operands are read from LDS
-// and step t's MFMAs run. A step ends with a wait for this wave's fetch of
-// step t+2 and a plain s_barrier (no memory fence: a fence would also wait
-// for the fetches still in flight).
+// K is walked in steps of 32 through a ring of four 32 KiB LDS stages, with
+// the two waves of each SIMD in ping-pong: waves 0-3 and waves 4-7 run the
+// same sequence one phase apart, alternating a memory phase (issue the
+// global -> LDS fetch of step t+3, read step t's operands from LDS into
+// registers) and a compute phase (step t's 32 MFMAs), so each SIMD's matrix
+// unit is fed by one wave while the other loads. Phases are separated by a
+// plain s_barrier of all 8 waves (no memory fence: a fence would also wait
+// for the fetches still in flight); a memory phase ends with a wait for this
+// wave's fetch of step t+1 and for its LDS reads.
 //
 // Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
 // 16 bytes at (LDS base + 16 l), so one wave instruction fills 1 KiB of LDS;
@@ -220,10 +224,12 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 // reach C rows or columns that are not stored.
 //
 // LDS layout of a stage (bytes):
-//   A [256 rows][4 chunks of 8 k], at 0: row r at 64 r; logical chunk c
-//     stored at chunk c ^ fa(r), fa(r) = ((r >> 1) ^ (r >> 3)) & 3. A
-//     fragment read (16 rows, one chunk per lane, ds_read_b128) then touches
-//     distinct banks whether the LDS serves 8 or 16 such lanes per cycle.
+//   A [16 blocks of 16 rows][4 chunks of 8 k][16 rows], at 0: chunk c of
+//     row r at 1024 (r / 16) + 256 c + 16 (r % 16). A fragment read (16 rows
+//     x one chunk per 16 lanes, ds_read_b128) is then 1 KiB read linearly
+//     (lane l at 16 l), which gfx950 serves without bank conflicts; row-major
+//     rows with any chunk swizzle measured 4 conflict cycles per read. One
+//     fetch instruction still covers 16 whole rows (64 bytes each).
 //   B [32 k rows][32 chunks of 8 n], at 16 KiB: k row kr at 512 kr; logical
 //     chunk c stored at chunk c ^ 2 tb(kr), tb(kr) = (kr & 3) | ((kr >> 3) & 3) << 2,
 //     i.e. 32-byte pairs XOR tb. B stays n-contiguous and is read with
@@ -238,9 +244,13 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 // C[m0 + l % 16][n0 + 4 (l / 16) + v], four consecutive columns, stored as
 // one 16-byte write.
 //
-// Tiles are handed out XCD by XCD (block b runs on XCD b % 8): each XCD gets
-// a contiguous run of tiles, ordered in groups of 8 tile rows, so the blocks
-// resident on one XCD share A and B panels in its L2.
+// Tiles are handed out in row-major order. The 256 blocks resident at a time
+// then cover a band of a few tile rows across all of N: A's band and all of
+// B (160 MiB at 8192^3) stay inside the 256 MiB MALL, and each XCD (block b
+// runs on XCD b % 8) holds every eighth tile column of the band. Measured
+// against grouped and XCD-remapped orders (A and B panels shared inside one
+// XCD's L2, but the XCDs spread over all of A), row-major was as fast or
+// faster at 8192^3.
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 #define MC_LDS __attribute__((address_space(3)))
@@ -251,14 +261,11 @@ constexpr int kFWaves = kFThreads / 64;
 constexpr int kFStages = 4;
 constexpr int kFStage = 32 * 1024;
 constexpr int kFBOffset = 16 * 1024;
-constexpr int kFGroupM = 8;
-constexpr int kXcds = 8;
 constexpr int kFRowFrags = 8;  // 16-row A fragments per wave (128 rows)
 constexpr int kFColFrags = 4;  // 16-column B fragments per wave (64 columns)
 // global_load_lds instructions per wave per step: 2 for A, 2 for B.
 constexpr int kFFetchPerStep = 4;
 
-__device__ __forceinline__ int swz_a(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 __device__ __forceinline__ int swz_b(int kr) { return (kr & 3) | (((kr >> 3) & 3) << 2); }
 
 // Per-lane addressing, set up once per block.
@@ -298,33 +305,18 @@ __device__ __forceinline__ u16x8 fast_read_b(const MC_LDS unsigned char* rd, con
     return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// One K step: fetch step `fetch_k` into `wr`; multiply the current operands
-// (av, bc) into acc row by row, and as each A fragment is used up read the
-// next step's A fragment into its place; read the next step's B fragments
-// into bn (B fragments stay live for the whole step). `rd` (the next step's
-// stage) and `wr` are distinct stages; declaring them __restrict__ gives the
-// LDS reads alias scopes that keep the compiler from making them wait for
-// the fetch.
-template <bool kBf16>
-__device__ __forceinline__ void fast_step(const MC_LDS unsigned char* __restrict__ rd, MC_LDS unsigned char* __restrict__ wr,
-                                          const FastLane& L, int fetch_k, u16x8 (&av)[kFRowFrags],
-                                          const u16x8 (&bc)[kFColFrags], u16x8 (&bn)[kFColFrags],
-                                          f32x4 (&acc)[kFRowFrags][kFColFrags]) {
+// Memory phase: fetch step `fetch_k` into `wr` and read the operands of the
+// step held in `rd` into (av, bv). `rd` and `wr` are distinct stages;
+// declaring them __restrict__ gives the LDS reads alias scopes that keep the
+// compiler from making them wait for the fetch.
+__device__ __forceinline__ void fast_memory_phase(const MC_LDS unsigned char* __restrict__ rd,
+                                                  MC_LDS unsigned char* __restrict__ wr, const FastLane& L, int fetch_k,
+                                                  u16x8 (&av)[kFRowFrags], u16x8 (&bv)[kFColFrags]) {
     fast_fetch(wr, L, fetch_k);
 #pragma unroll
-    for (int fi = 0; fi < kFRowFrags; ++fi) {
+    for (int f = 0; f < kFRowFrags; ++f) av[f] = fast_read_a(rd, L, f);
 #pragma unroll
-        for (int fj = 0; fj < kFColFrags; ++fj) acc[fi][fj] = mfma<kBf16>(bc[fj], av[fi], acc[fi][fj]);
-        av[fi] = fast_read_a(rd, L, fi);
-        if (fi < kFColFrags) bn[fi] = fast_read_b(rd, L, fi);
-    }
-}
-
-// s_waitcnt with vmcnt = n (n < 16) and expcnt / lgkmcnt left alone.
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 16, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | n);
+    for (int f = 0; f < kFColFrags; ++f) bv[f] = fast_read_b(rd, L, f);
 }
 
 // A workgroup barrier without a memory fence; the compiler may not move
@@ -347,30 +339,20 @@ __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigne
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
 
-    // Tile of this block.
-    const int tiles_m = (m + kFBM - 1) / kFBM, tiles_n = (n + kFBN - 1) / kFBN;
-    const int blocks = static_cast<int>(gridDim.x);
-    int id = static_cast<int>(blockIdx.x);
-    if (blocks % kXcds == 0) id = (id % kXcds) * (blocks / kXcds) + id / kXcds;
-    const int per_group = kFGroupM * tiles_n;
-    const int group = id / per_group;
-    const int first_m = group * kFGroupM;
-    const int rows_in_group = min(tiles_m - first_m, kFGroupM);
-    const int in_group = id - group * per_group;
-    const int tm = first_m + in_group % rows_in_group;
-    const int tn = in_group / rows_in_group;
+    // Tile of this block (row-major).
+    const int tiles_n = (n + kFBN - 1) / kFBN;
+    const int tm = static_cast<int>(blockIdx.x) / tiles_n, tn = static_cast<int>(blockIdx.x) % tiles_n;
     const int row0 = tm * kFBM, col0 = tn * kFBN;
 
     FastLane L;
     L.wave = wave;
-    // A: wave w fills rows 32 w .. 32 w + 31, sixteen rows per instruction;
-    // lane -> (row 32 w + 16 i + l / 4, physical chunk l % 4).
+    // A: wave w fills the 16-row blocks 2 w and 2 w + 1, one per
+    // instruction; lane -> (row 32 w + 16 i + l % 16, chunk l / 16).
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int r = wave * 32 + i * 16 + (lane >> 2);
-        const int lc = (lane & 3) ^ swz_a(r);
+        const int r = wave * 32 + i * 16 + (lane & 15);
         const int gr = min(row0 + r, m - 1);
-        L.a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + lc * 8;
+        L.a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + (lane >> 4) * 8;
     }
     // B: wave w fills k rows 4 w .. 4 w + 3, two per instruction; lane ->
     // (k row 4 w + 2 i + l / 32, physical chunk l % 32).
@@ -386,10 +368,7 @@ __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigne
     const int wr = (wave >> 2) * 128, wc = (wave & 3) * 64;
     const int li = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) {
-        const int r = wr + f * 16 + li;
-        L.a_off[f] = r * 64 + ((g ^ swz_a(r)) << 4);
-    }
+    for (int f = 0; f < kFRowFrags; ++f) L.a_off[f] = (wr + f * 16) * 64 + lane * 16;
     // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
     // k row 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
     const int te = (lane & 15) >> 2, tc = lane & 3;
@@ -411,32 +390,33 @@ __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigne
 
     const int steps = k / kFBK;
     auto stage = [&](int t) { return lds + (t & (kFStages - 1)) * kFStage; };
-    u16x8 av[kFRowFrags], b0[kFColFrags], b1[kFColFrags];
-    // Prologue: steps 0..2 in flight, then step 0 landed and read.
+    u16x8 av[kFRowFrags], bv[kFColFrags];
+    // Prologue: steps 0..2 landed.
     const int pre = min(steps, kFStages - 1);
     for (int t = 0; t < pre; ++t) fast_fetch(stage(t), L, t * kFBK);
     __builtin_amdgcn_s_waitcnt(0);
     step_barrier();
-#pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) av[f] = fast_read_a(stage(0), L, f);
-#pragma unroll
-    for (int f = 0; f < kFColFrags; ++f) b0[f] = fast_read_b(stage(0), L, f);
+    // Waves 4-7 start one phase late.
+    const bool late = wave >= kFWaves / 2;
+    if (late) step_barrier();
 
-    // Steady state, two steps per trip so the B registers alternate without
-    // copies. Every step fetches: past the last step it fetches the last step
-    // again, into the stage of step t-1, which no wave reads any more; every
-    // step reads: past the last step it reads a stage whose values are never
-    // used. So each step ends with this wave's fetches of steps t+2 and t+3
-    // outstanding, and waits for the older one.
+    // Every memory phase fetches: past the last step it fetches the last step
+    // again, into the stage of step t-1, which no wave reads any more. After
+    // the fetch of step t+3 this wave has the fetches of steps t+1..t+3 in
+    // flight and waits for the oldest, which the other group reads two
+    // phases later.
     const int last = (steps - 1) * kFBK;
-    for (int t = 0; t < steps; t += 2) {
-        fast_step<kBf16>(stage(t + 1), stage(t + 3), L, min((t + 3) * kFBK, last), av, b0, b1, acc);
-        wait_vmcnt<kFFetchPerStep>();
+    for (int t = 0; t < steps; ++t) {
+        fast_memory_phase(stage(t), stage(t + 3), L, min((t + 3) * kFBK, last), av, bv);
+        __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kFFetchPerStep));  // vmcnt(8), lgkmcnt(0)
         step_barrier();
-        fast_step<kBf16>(stage(t + 2), stage(t + 4), L, min((t + 4) * kFBK, last), av, b1, b0, acc);
-        wait_vmcnt<kFFetchPerStep>();
+#pragma unroll
+        for (int fi = 0; fi < kFRowFrags; ++fi)
+#pragma unroll
+            for (int fj = 0; fj < kFColFrags; ++fj) acc[fi][fj] = mfma<kBf16>(bv[fj], av[fi], acc[fi][fj]);
         step_barrier();
     }
+    if (!late) step_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
     // acc[fi][fj] holds C[row0 + wr + 16 fi + l % 16][col0 + wc + 16 fj + 4 (l / 16) + v].

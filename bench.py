@@ -8,8 +8,10 @@ pass over one batch of synthetic, seeded input already resident in HBM).
 The headline workload is BASELINE config 2, the fp32 MLP block
 (mlp_gelu.mcg) at B=8192: GEMM, fused bias+GELU, GEMM, fused
 bias+residual. W untimed steps, then exactly K timed steps between two HIP
-events on the executable's stream, with a HIP event before every launch so
-each kernel's duration comes from the same timed region.
+events on the executable's stream. Each kernel's duration is then measured
+in the same process on the same stream: the launch alone, back to back,
+between one pair of HIP events (events between launches would add their own
+gaps to short kernels).
 
 Prints ONE JSON line. `value` is the step's GEMM throughput (TFLOP/s = the
 two GEMMs' 2MNK FLOPs per step / ms_per_step). `roofline` is for the
@@ -81,10 +83,13 @@ def rate_entry(name: str, work: dict, ms: float, gemm_peak: float = PEAK_FP32_TF
             "frac": gbs / PEAK_HBM_GBS}
 
 
-def time_graph(mc, compiled, steps: int, warmup: int, rotations=None) -> dict:
-    """W warmup steps, then K steps timed between HIP events with per-launch
-    events. `rotations`: list of (input_ptrs, output_ptrs) bound in turn, so
-    consecutive steps touch different buffers (defeats the 256 MB MALL)."""
+def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None) -> dict:
+    """W warmup steps, then K steps timed between one pair of HIP events on
+    the executable's stream (ms_per_step). Then each launch of the step alone,
+    `reps` times back to back between one pair of HIP events on that stream
+    (its mean duration, with no event between launches to perturb it).
+    `rotations`: list of (input_ptrs, output_ptrs) bound in turn, so
+    consecutive launches touch different buffers (defeats the 256 MB MALL)."""
     def bind(i):
         if rotations:
             ins, outs = rotations[i % len(rotations)]
@@ -96,20 +101,32 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None) -> dict:
         bind(i)
         compiled.enqueue()
     compiled.synchronize()
-    compiled.profile_start(steps)
     start, stop = mc.Event(), mc.Event()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(steps):
         bind(i)
-        compiled.enqueue_profiled()
+        compiled.enqueue()
     stop.record(stream)
     compiled.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_ms(stop)
-    per_launch = compiled.profile_read()  # [steps, launches]
-    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall,
-            "launch_ms": per_launch.mean(axis=0).tolist(), "launch_ms_min": per_launch.min(axis=0).tolist()}
+    reps = reps or max(steps, 10)
+    launch_ms = []
+    for j in range(compiled.kernel_launches):
+        for i in range(2):
+            bind(i)
+            compiled.enqueue_launch(j)
+        start.record(stream)
+        for i in range(reps):
+            bind(i)
+            compiled.enqueue_launch(j)
+        stop.record(stream)
+        compiled.synchronize()
+        launch_ms.append(start.elapsed_ms(stop) / reps)
+    bind(0)
+    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "launch_ms": launch_ms,
+            "launch_reps": reps}
 
 
 def bench_mlp(mc, batch: int, steps: int, warmup: int) -> dict:
@@ -142,20 +159,22 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
     work = node_work(c.graph())
     (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
     return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
-            "gbs": k["gbs"], "frac": k["frac"], "launch_ms_min": t["launch_ms_min"][0]}
+            "gbs": k["gbs"], "frac": k["frac"]}
 
 
 def time_gemm(mc, launch, steps: int, warmup: int) -> float:
+    """Mean duration of `steps` back-to-back launches between one pair of HIP
+    events on their stream."""
     s = mc.Stream()
     for _ in range(warmup):
         launch(s)
-    evs = [mc.Event() for _ in range(steps + 1)]
-    evs[0].record(s)
-    for i in range(steps):
+    start, stop = mc.Event(), mc.Event()
+    start.record(s)
+    for _ in range(steps):
         launch(s)
-        evs[i + 1].record(s)
+    stop.record(s)
     s.synchronize()
-    return float(np.median([evs[i].elapsed_ms(evs[i + 1]) for i in range(steps)]))
+    return start.elapsed_ms(stop) / steps
 
 
 def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]:

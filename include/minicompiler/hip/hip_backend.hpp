@@ -61,6 +61,14 @@ struct HipOptions {
     MatmulKernel matmul = MatmulKernel::Auto;
     // 16-byte loads and stores in elementwise kernels when the layout allows.
     bool vectorize = true;
+    // Elementwise kernel shape: vectors (or floats) each lane has in flight
+    // per loop step, non-temporal hints on the streaming loads and stores,
+    // and resident blocks per CU the grid is sized for (0: the occupancy
+    // the runtime reports).
+    unsigned elementwise_items = 4;
+    bool nontemporal_loads = true;
+    bool nontemporal_stores = true;
+    unsigned elementwise_blocks_per_cu = 0;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).
@@ -104,6 +112,8 @@ public:
     // enqueue() with events[j] recorded before launch j and events[launches]
     // after the last one (kernel_launches() + 1 hipEvent_t handles).
     virtual Status enqueue_with_events(void* stream, void* const* events) = 0;
+    // Launch j of the list alone (for timing one kernel back to back).
+    virtual Status enqueue_launch(std::size_t j, void* stream = nullptr) = 0;
     virtual Status synchronize() = 0;
     // Waits for the device, then copies the outputs to the host.
     virtual Status download_outputs(const std::vector<float*>& host_outputs) = 0;

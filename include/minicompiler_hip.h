@@ -101,6 +101,9 @@ MC_API int mc_profile_start(void* handle, int steps);
 MC_API int mc_enqueue_profiled(void* handle, void* stream);
 MC_API int mc_profile_read(void* handle, float* ms, int capacity);
 MC_API int mc_launch_names(void* handle, char* out, int size);
+/* Launch j of the executable's launch list alone on `stream` (NULL: its own
+ * stream), e.g. to time one kernel back to back without events between. */
+MC_API int mc_enqueue_launch(void* handle, int j, void* stream);
 
 /* The library's seeded generators (random.hpp; fill_uniform is the
  * reference's src/random.cpp:15-26), for callers that build inputs. */

@@ -82,6 +82,7 @@ _SIGNATURES = {
     "mc_arena_bytes": (_ll, [_vp]),
     "mc_profile_start": (_i, [_vp, _i]),
     "mc_enqueue_profiled": (_i, [_vp, _vp]),
+    "mc_enqueue_launch": (_i, [_vp, _i, _vp]),
     "mc_profile_read": (_i, [_vp, _fp, _i]),
     "mc_launch_names": (_i, [_vp, _cp, _i]),
     "mc_fill_uniform": (None, [_fp, _sz, _c.c_ulonglong, _f, _f]),
@@ -381,6 +382,9 @@ class Compiled:
 
     def profile_start(self, steps: int) -> None:
         _check_graph(library().mc_profile_start(self._h, steps), "mc_profile_start")
+
+    def enqueue_launch(self, j: int, stream=None) -> None:
+        _check_graph(library().mc_enqueue_launch(self._h, j, _stream_handle(stream)), "mc_enqueue_launch")
 
     def enqueue_profiled(self, stream=None) -> None:
         _check_graph(library().mc_enqueue_profiled(self._h, _stream_handle(stream)), "mc_enqueue_profiled")

@@ -110,8 +110,20 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             Result<long long> d = to_integer(value);
             if (!d.ok()) return d.error();
             o.device = static_cast<int>(d.value());
+        } else if (key == "ew_items" || key == "ew_blocks_per_cu") {
+            Result<long long> v = to_integer(value);
+            if (!v.ok()) return v.error();
+            if (v.value() < 0 || v.value() > 64 || (key == "ew_items" && v.value() < 1)) {
+                return Error{"option " + key + " out of range: " + value};
+            }
+            (key == "ew_items" ? o.elementwise_items : o.elementwise_blocks_per_cu) = static_cast<unsigned>(v.value());
+        } else if (key == "ew_nt_loads") {
+            o.nontemporal_loads = value != "0" && value != "false";
+        } else if (key == "ew_nt_stores") {
+            o.nontemporal_stores = value != "0" && value != "false";
         } else {
-            return Error{"unknown option '" + key + "' (matmul, vectorize, device)"};
+            return Error{"unknown option '" + key +
+                         "' (matmul, vectorize, device, ew_items, ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
         }
     }
     return o;
@@ -365,6 +377,14 @@ MC_API int mc_enqueue(void* h, void* stream) {
     return st.ok() ? 0 : fail(st.message());
 }
 
+MC_API int mc_enqueue_launch(void* h, int j, void* stream) {
+    Compiled* c = as_compiled(h);
+    if (!c->exe) return fail("mc_enqueue_launch: no executable");
+    if (j < 0) return fail("mc_enqueue_launch: negative launch index");
+    Status st = c->exe->enqueue_launch(static_cast<std::size_t>(j), stream);
+    return st.ok() ? 0 : fail(st.message());
+}
+
 MC_API int mc_download(void* h, float* const* outputs) {
     Compiled* c = as_compiled(h);
     if (!c->exe) return fail("mc_download: no executable");
@@ -603,8 +623,7 @@ MC_API int mc_kernel_sources(const void* h, char* out, int size) {
     if (c->exe) {
         sources = c->exe->kernel_sources();
     } else {
-        hip::CodegenOptions cg;
-        cg.allow_vectorize = c->options.vectorize;
+        const hip::CodegenOptions cg = hip::codegen_options(c->options);
         for (const Node& n : c->graph.nodes()) {
             if (!is_elementwise(n.op) && n.op != OpKind::FusedElementwise) continue;
             const FusedProgram p = n.op == OpKind::FusedElementwise ? *n.fused : hip::single_op_program(n.op);

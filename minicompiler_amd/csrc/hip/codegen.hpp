@@ -13,6 +13,7 @@
 // patterns, and scalar inputs are loaded once per lane before the loop.
 
 #include "minicompiler/fused_program.hpp"
+#include "minicompiler/hip/hip_backend.hpp"
 #include "minicompiler/tensor.hpp"
 
 #include <cstddef>
@@ -32,7 +33,7 @@ struct CodegenOptions {
     // bytes in flight per wave to cover HBM latency.
     unsigned items_per_lane = 4;
     // Non-temporal hints on the streaming loads and stores.
-    bool nontemporal_loads = false;
+    bool nontemporal_loads = true;
     bool nontemporal_stores = true;
 };
 
@@ -61,6 +62,9 @@ Access classify_access(const Shape& in, const Shape& out);
 
 ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const std::vector<Shape>& input_shapes,
                                               const Shape& out_shape, const CodegenOptions& options = {});
+
+// The generator options a compiled graph uses.
+CodegenOptions codegen_options(const HipOptions& options);
 
 // One unary or binary op as a program (load the operands, apply the op), so
 // unfused graphs go through the same generator.

@@ -205,19 +205,8 @@ public:
         std::size_t j = 0;
         for (Launch& l : launches_) {
             if (events) MCHIP_TRY(mchip_event_record(events[j++], s));
-            if (l.kind == Launch::Kind::Elementwise) {
-                const int rc = mchip_module_launch(l.function, l.grid, kElementwiseBlock, 0, s, l.params.data());
-                if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel");
-            } else {
-                const int rc = mchip_launch_matmul(static_cast<int>(l.matmul), static_cast<const float*>(value_ptr(a_of(l))),
-                                                   static_cast<const float*>(value_ptr(b_of(l))),
-                                                   static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, l.splits,
-                                                   l.workspace);
-                if (rc != 0) {
-                    return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " +
-                                 mchip_error_string(rc)};
-                }
-            }
+            Status st = launch(l, s);
+            if (!st.ok()) return st;
         }
         if (events) MCHIP_TRY(mchip_event_record(events[j], s));
         // Graph outputs that are inputs or constants: copy into bound memory.
@@ -227,6 +216,11 @@ public:
             MCHIP_TRY(mchip_memcpy_dtod_async(output_bound_[k], value_ptr(id), graph_.node(id).type.size_bytes(), s));
         }
         return Status();
+    }
+
+    Status enqueue_launch(std::size_t j, void* stream) override {
+        if (j >= launches_.size()) return Error{"launch " + std::to_string(j) + " out of range"};
+        return launch(launches_[j], stream ? stream : stream_);
     }
 
     Status synchronize() override {
@@ -311,6 +305,21 @@ public:
     std::size_t arena_bytes() const override { return arena_bytes_; }
 
 private:
+    Status launch(Launch& l, void* s) {
+        if (l.kind == Launch::Kind::Elementwise) {
+            const int rc = mchip_module_launch(l.function, l.grid, kElementwiseBlock, 0, s, l.params.data());
+            return rc == 0 ? Status() : hip_status(rc, "hipModuleLaunchKernel");
+        }
+        const int rc = mchip_launch_matmul(static_cast<int>(l.matmul), static_cast<const float*>(value_ptr(a_of(l))),
+                                           static_cast<const float*>(value_ptr(b_of(l))),
+                                           static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, l.splits,
+                                           l.workspace);
+        if (rc != 0) {
+            return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " + mchip_error_string(rc)};
+        }
+        return Status();
+    }
+
     NodeId a_of(const Launch& l) const { return graph_.node(l.node).inputs[0]; }
     NodeId b_of(const Launch& l) const { return graph_.node(l.node).inputs[1]; }
 
@@ -343,8 +352,7 @@ private:
             ElementwiseKernel kernel;
         };
         std::vector<Job> jobs;
-        CodegenOptions cg;
-        cg.allow_vectorize = options_.vectorize;
+        const CodegenOptions cg = codegen_options(options_);
         for (std::size_t j = 0; j < launches_.size(); ++j) {
             if (launches_[j].kind != Launch::Kind::Elementwise) continue;
             const Node& node = graph_.node(launches_[j].node);
@@ -382,6 +390,9 @@ private:
             l.count = static_cast<unsigned>(kern.vectorized ? numel / 4 : numel);
             int per_cu = 0;
             MCHIP_TRY(mchip_occupancy(&per_cu, l.function, static_cast<int>(kElementwiseBlock), 0));
+            if (options_.elementwise_blocks_per_cu > 0) {
+                per_cu = std::min(per_cu, static_cast<int>(options_.elementwise_blocks_per_cu));
+            }
             const std::size_t per_step = kern.items_per_block_step();
             const std::size_t needed = (static_cast<std::size_t>(l.count) + per_step - 1) / per_step;
             const std::size_t resident = std::max<std::size_t>(1, static_cast<std::size_t>(per_cu) * device_.cu_count);

@@ -37,7 +37,8 @@ def test_fused_gelu_is_one_vectorised_kernel(mc):
     # Exact bit patterns, once, in the program (before the kernel's loop).
     assert src.count("__uint_as_float(0x3f000000u)") == 1
     assert src.index("0x3f000000u") < kernel_loop(src)
-    assert src.count("tanhf(") == 1               # once in the program ...
+    assert src.count("mc_tanh(r") == 1            # once in the program ...
+    assert src.count("float mc_tanh(float x)") == 1  # (the generator's own tanh, defined once)
     assert src.count("mc_program(a0[u].") == 8     # ... applied to 4 lanes, full and ragged steps
 
 

@@ -64,6 +64,24 @@ def test_unary_ops_match_the_cpu_oracle(device, mc, oracle, op, shape):
     assert_close(gpu[0], ref[0], 0.0 if exact else TRANS_RTOL, 0.0 if exact else TRANS_ATOL, f"{op} vs double")
 
 
+def test_tanh_over_a_dense_range_and_its_special_values(device, mc, oracle):
+    # The generated kernels' own tanh (a polynomial below |x| = 0.625, exp2
+    # and a reciprocal above) against the double evaluator, at the unary
+    # tolerance; the threshold, tiny and huge values, +-0, +-inf and NaN.
+    xs = np.concatenate([np.linspace(-12, 12, 48001, dtype=np.float32),
+                         np.float32(0.625) * np.array([1 - 2**-23, 1, 1 + 2**-23], np.float32),
+                         -np.float32(0.625) * np.array([1 - 2**-23, 1, 1 + 2**-23], np.float32),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 1e-45, 2**-20, 45.0, -45.0, 1e30, -1e30], np.float32),
+                         np.array([np.inf, -np.inf], np.float32)]).astype(np.float32)
+    c = mc.Compiled(unary_graph("tanh", (xs.size,)))
+    gpu = c.run([xs])[0]
+    ref = oracle.evaluate_compiled(c, [xs], mode="reference")[0]
+    assert_close(gpu, ref, TRANS_RTOL, TRANS_ATOL, "tanh")
+    assert np.array_equal(np.signbit(gpu[xs == 0]), np.signbit(xs[xs == 0]))  # -0 stays -0
+    c4 = mc.Compiled(unary_graph("tanh", (4,)))
+    assert np.all(np.isnan(c4.run([np.full(4, np.nan, np.float32)])[0]))
+
+
 @pytest.mark.parametrize("sa,sb", PATTERNS)
 def test_binary_ops_match_bit_for_bit_for_every_broadcast_pattern(device, mc, oracle, sa, sb):
     for op in BINARY:

@@ -49,21 +49,24 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def node_work(graph: dict) -> list[dict]:
-    """Algorithmic work of each launch (compute nodes in id order): 2MNK FLOPs
-    for a matmul; for an elementwise kernel the bytes of its output plus each
+def node_work(graph: dict, launch_nodes=None) -> list[dict]:
+    """Algorithmic work of each launch: 2MNK FLOPs for a matmul (also one
+    whose store applies a fused elementwise group: it is bound by the matrix
+    cores); for an elementwise kernel the bytes of its output plus each
     distinct non-scalar operand read once (the reference's bytes_moved,
-    bench/bench_cuda.cpp:79-95)."""
+    bench/bench_cuda.cpp:79-95). `launch_nodes`: the node ids each launch
+    computes (default: one launch per compute node, in id order)."""
     nodes = graph["nodes"]
+    if launch_nodes is None:
+        launch_nodes = [[n["id"]] for n in nodes if n["op_name"] not in ("input", "const")]
+    size = lambda s: int(np.prod(s, dtype=np.int64)) if s else 1
     out = []
-    for n in nodes:
-        if n["op_name"] in ("input", "const"):
-            continue
+    for ids in launch_nodes:
+        n = nodes[ids[0]]
         if n["op_name"] == "matmul":
             (m, k), (_, nn) = nodes[n["inputs"][0]]["shape"], nodes[n["inputs"][1]]["shape"]
-            out.append({"kind": "gemm", "flop": 2.0 * m * nn * k, "m": m, "n": nn, "k": k})
+            out.append({"kind": "gemm", "flop": 2.0 * m * nn * k, "m": m, "n": nn, "k": k, "fused": len(ids) > 1})
         else:
-            size = lambda s: int(np.prod(s, dtype=np.int64)) if s else 1
             b = 4 * size(n["shape"])
             for i in sorted(set(n["inputs"])):
                 sz = size(nodes[i]["shape"])
@@ -134,7 +137,7 @@ def bench_mlp(mc, batch: int, steps: int, warmup: int) -> dict:
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
     t = time_graph(mc, c, steps, warmup)
-    work = node_work(c.graph())
+    work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
     flop = sum(w["flop"] for w in work if w["kind"] == "gemm")
@@ -156,7 +159,7 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
         bufs.append((bi, bo))
     rot = [([bi.ptr], [bo.ptr]) for bi, bo in bufs]
     t = time_graph(mc, c, steps, warmup, rot)
-    work = node_work(c.graph())
+    work = node_work(c.graph(), c.launch_nodes)
     (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
     return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
             "gbs": k["gbs"], "frac": k["frac"]}

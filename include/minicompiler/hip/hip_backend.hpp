@@ -69,6 +69,10 @@ struct HipOptions {
     bool nontemporal_loads = true;
     bool nontemporal_stores = true;
     unsigned elementwise_blocks_per_cu = 0;
+    // Apply a fused elementwise group that consumes a matmul's product in
+    // the store of an FP32 matrix-core GEMM (one kernel instead of two), when
+    // the memory plan makes that safe.
+    bool fuse_epilogue = true;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).
@@ -132,6 +136,9 @@ public:
     virtual std::vector<std::string> kernel_sources() const = 0;
     // One label per launch: "matmul <kernel> MxNxK" or "<op> <node> f32[...]".
     virtual std::vector<std::string> launch_names() const = 0;
+    // The graph nodes each launch computes (a fused matmul: the matmul and
+    // its epilogue group).
+    virtual std::vector<std::vector<NodeId>> launch_nodes() const = 0;
     virtual std::vector<MatmulKernel> matmul_kernels() const = 0;
     virtual double jit_compile_ms() const = 0;
     virtual std::size_t arena_bytes() const = 0;

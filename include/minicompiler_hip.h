@@ -70,7 +70,9 @@ MC_API void mc_release(void* handle); /* capi.cpp:233-235 */
 /* ---- Part 2: extensions ---------------------------------------------------- */
 
 /* mc_compile from graph text, with backend options
- * "matmul=NAME,vectorize=0|1,device=N" (NULL or "" for defaults). */
+ * "matmul=NAME,vectorize=0|1,device=N,epilogue=0|1" and the elementwise
+ * kernel shape "ew_items=N,ew_nt_loads=0|1,ew_nt_stores=0|1,
+ * ew_blocks_per_cu=N" (NULL or "" for defaults). */
 MC_API void* mc_compile_source(const char* text, const char* dims, const char* passes, const char* backend,
                                const char* options, char* error, int error_size);
 /* The message of this thread's last failed call. */
@@ -104,6 +106,9 @@ MC_API int mc_launch_names(void* handle, char* out, int size);
 /* Launch j of the executable's launch list alone on `stream` (NULL: its own
  * stream), e.g. to time one kernel back to back without events between. */
 MC_API int mc_enqueue_launch(void* handle, int j, void* stream);
+/* The graph nodes each launch computes, launches separated by ';' and nodes
+ * by ',' (a matmul with a fused epilogue lists the matmul, then the group). */
+MC_API int mc_launch_nodes(void* handle, char* out, int size);
 
 /* The library's seeded generators (random.hpp; fill_uniform is the
  * reference's src/random.cpp:15-26), for callers that build inputs. */
@@ -132,6 +137,12 @@ MC_API int mc_print_graph(const void* handle, char* out, int size);
 MC_API int mc_generate_elementwise_kernel(const char* program, const char* input_shapes, const char* out_shape,
                                           int allow_vectorize, int items_per_lane, int* vectorized, char* out,
                                           int size);
+/* The FP32 matrix-core GEMM whose store applies `program` (its input
+ * `acc_input` is the accumulated value; the others are read by access class
+ * against `out_shape`), as the executable generates it for a matmul with a
+ * fused elementwise consumer. Works without a device. */
+MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
+                                            const char* out_shape, int vectorized_operands, char* out, int size);
 /* hipRTC-compiles `source` for `arch` (e.g. "gfx950") to a code object with
  * the generator's options; no device needed. Returns 0 or 1; the log goes to
  * `log`. */

@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mc_profile_start": (_i, [_vp, _i]),
     "mc_enqueue_profiled": (_i, [_vp, _vp]),
     "mc_enqueue_launch": (_i, [_vp, _i, _vp]),
+    "mc_launch_nodes": (_i, [_vp, _cp, _i]),
     "mc_profile_read": (_i, [_vp, _fp, _i]),
     "mc_launch_names": (_i, [_vp, _cp, _i]),
     "mc_fill_uniform": (None, [_fp, _sz, _c.c_ulonglong, _f, _f]),
@@ -95,6 +96,7 @@ _SIGNATURES = {
     "mc_print_graph": (_i, [_vp, _cp, _i]),
     "mc_generate_elementwise_kernel": (_i, [_cp, _cp, _cp, _i, _i, _c.POINTER(_i), _cp, _i]),
     "mc_compile_kernel_source": (_i, [_cp, _cp, _cp, _i]),
+    "mc_generate_gemm_epilogue_kernel": (_i, [_cp, _i, _cp, _cp, _i, _cp, _i]),
     "mc_launch_matmul": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "mc_launch_matmul_lowp": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "mc_convert_f32": (_i, [_i, _vp, _vp, _sz, _vp]),
@@ -433,6 +435,12 @@ class Compiled:
         return [s for s in buf.value.decode().split(",") if s]
 
     @property
+    def launch_nodes(self) -> list[list[int]]:
+        """Graph node ids each launch computes (a fused matmul: matmul, group)."""
+        text = _text_call(library().mc_launch_nodes, self._h)
+        return [[int(x) for x in part.split(",")] for part in text.split(";") if part]
+
+    @property
     def kernel_sources(self) -> list[str]:
         text = _text_call(library().mc_kernel_sources, self._h)
         return [s for s in text.split("//----\n") if s] if text else []
@@ -565,6 +573,14 @@ def generate_elementwise_kernel(program: str, input_shapes: Sequence[Sequence[in
     lib.mc_generate_elementwise_kernel(program.encode(), shapes.encode(), out.encode(), int(allow_vectorize),
                                        items_per_lane, ctypes.byref(vec), buf, n + 1)
     return buf.value.decode(), bool(vec.value)
+
+
+def generate_gemm_epilogue_kernel(program: str, acc_input: int, input_shapes: Sequence[Sequence[int]],
+                                  out_shape: Sequence[int], vectorized_operands: bool = True) -> str:
+    shapes = ";".join("[" + ",".join(str(d) for d in s) + "]" for s in input_shapes)
+    out = "[" + ",".join(str(d) for d in out_shape) + "]"
+    args = (program.encode(), acc_input, shapes.encode(), out.encode(), int(vectorized_operands))
+    return _text_call(library().mc_generate_gemm_epilogue_kernel, *args)
 
 
 def compile_kernel_source(source: str, arch: str = "gfx950") -> tuple[bool, str]:

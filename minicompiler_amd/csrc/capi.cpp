@@ -4,6 +4,7 @@
 #include "minicompiler_hip.h"
 
 #include "hip/codegen.hpp"
+#include "hip/rtc_sources.hpp"
 #include "hip/hip_rt.h"
 #include "hip/kernel_compiler.hpp"
 #include "hip/matmul.h"
@@ -117,13 +118,15 @@ Result<hip::HipOptions> parse_options(const char* spec) {
                 return Error{"option " + key + " out of range: " + value};
             }
             (key == "ew_items" ? o.elementwise_items : o.elementwise_blocks_per_cu) = static_cast<unsigned>(v.value());
+        } else if (key == "epilogue") {
+            o.fuse_epilogue = value != "0" && value != "false";
         } else if (key == "ew_nt_loads") {
             o.nontemporal_loads = value != "0" && value != "false";
         } else if (key == "ew_nt_stores") {
             o.nontemporal_stores = value != "0" && value != "false";
         } else {
             return Error{"unknown option '" + key +
-                         "' (matmul, vectorize, device, ew_items, ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
+                         "' (matmul, vectorize, device, epilogue, ew_items, ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
         }
     }
     return o;
@@ -375,6 +378,17 @@ MC_API int mc_enqueue(void* h, void* stream) {
     if (!c->exe) return fail("mc_enqueue: no executable");
     Status st = c->exe->enqueue(stream);
     return st.ok() ? 0 : fail(st.message());
+}
+
+MC_API int mc_launch_nodes(void* h, char* out, int size) {
+    const Compiled* c = as_compiled(h);
+    if (!c->exe) return fail("mc_launch_nodes: no executable");
+    std::string text;
+    for (const std::vector<NodeId>& ids : c->exe->launch_nodes()) {
+        if (!text.empty()) text += ';';
+        for (std::size_t k = 0; k < ids.size(); ++k) text += (k ? "," : "") + std::to_string(ids[k]);
+    }
+    return copy_text(out, size, text);
 }
 
 MC_API int mc_enqueue_launch(void* h, int j, void* stream) {
@@ -661,6 +675,31 @@ MC_API int mc_generate_elementwise_kernel(const char* program, const char* input
     if (items_per_lane > 0) cg.items_per_lane = static_cast<unsigned>(items_per_lane);
     const hip::ElementwiseKernel k = hip::generate_elementwise_kernel(p.value(), shapes, os.value(), cg);
     if (vectorized) *vectorized = k.vectorized ? 1 : 0;
+    return copy_text(out, size, k.source);
+}
+
+MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
+                                            const char* out_shape, int vectorized_operands, char* out, int size) {
+    Result<FusedProgram> p = parse_program(program ? program : "");
+    if (!p.ok()) return fail(p.error().message), -1;
+    std::vector<Shape> shapes;
+    std::stringstream list(input_shapes ? input_shapes : "");
+    for (std::string item; std::getline(list, item, ';');) {
+        if (item.find('[') == std::string::npos) continue;
+        Result<Shape> s = parse_shape(item);
+        if (!s.ok()) return fail(s.error().message), -1;
+        shapes.push_back(s.value());
+    }
+    Result<Shape> os = parse_shape(out_shape ? out_shape : "");
+    if (!os.ok()) return fail(os.error().message), -1;
+    Status st = validate(p.value(), shapes.size());
+    if (!st.ok()) return fail(st.message()), -1;
+    if (acc_input < 0 || static_cast<std::size_t>(acc_input) >= shapes.size()) {
+        return fail("mc_generate_gemm_epilogue_kernel: acc_input out of range"), -1;
+    }
+    const hip::GemmEpilogueKernel k = hip::generate_gemm_epilogue_kernel(
+        p.value(), static_cast<std::size_t>(acc_input), shapes, os.value(), vectorized_operands != 0,
+        hip::kGemmF32MfmaSource);
     return copy_text(out, size, k.source);
 }
 

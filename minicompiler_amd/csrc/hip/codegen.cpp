@@ -90,6 +90,31 @@ const char* const kTanhSource = R"(__device__ __forceinline__ float mc_tanh(floa
 
 )";
 
+// The program as a device function of its inputs' floats: one `const
+// float` per instruction, so with -ffp-contract=off every op rounds to float.
+std::string program_function(const FusedProgram& program, std::size_t num_inputs) {
+    std::ostringstream os;
+    os << "__device__ __forceinline__ float mc_program(";
+    for (std::size_t k = 0; k < num_inputs; ++k) os << (k ? ", " : "") << "float x" << k;
+    if (num_inputs == 0) os << "void";
+    os << ")\n{\n";
+    for (std::size_t r = 0; r < program.instrs.size(); ++r) {
+        const FusedInstr& ins = program.instrs[r];
+        os << "\tconst float r" << r << " = ";
+        switch (ins.kind) {
+            case FusedInstr::Kind::Load: os << "x" << ins.a; break;
+            case FusedInstr::Kind::Immediate: os << exact_float(ins.immediate); break;
+            case FusedInstr::Kind::Unary: os << op_text(ins.op, "r" + std::to_string(ins.a), ""); break;
+            case FusedInstr::Kind::Binary:
+                os << op_text(ins.op, "r" + std::to_string(ins.a), "r" + std::to_string(ins.b));
+                break;
+        }
+        os << ";\n";
+    }
+    os << "\treturn r" << program.instrs.size() - 1 << ";\n}\n\n";
+    return os.str();
+}
+
 }  // namespace
 
 Access classify_access(const Shape& in, const Shape& out) {
@@ -123,6 +148,60 @@ Access classify_access(const Shape& in, const Shape& out) {
         expr += (expr.empty() ? "" : " + ") + coord;
     }
     return {Access::Kind::General, 0, expr};
+}
+
+GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
+                                                 const std::vector<Shape>& input_shapes, const Shape& out_shape,
+                                                 bool vectorized_operands, const char* gemm_body_source) {
+    const std::size_t num_inputs = input_shapes.size();
+    std::ostringstream os;
+    os << "// minicompiler-hip FP32 GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
+       << to_string(out_shape) << ".\n";
+    os << gemm_body_source << "\n";
+    if (uses_op(program, OpKind::Tanh)) os << kTanhSource;
+    os << program_function(program, num_inputs);
+    // Index helpers of General inputs, in terms of the flat output index i.
+    for (std::size_t k = 0; k < num_inputs; ++k) {
+        if (k == acc_input) continue;
+        const Access a = classify_access(input_shapes[k], out_shape);
+        if (a.kind == Access::Kind::General) {
+            os << "__device__ __forceinline__ unsigned mc_general_" << k << "(unsigned i) { return " << a.index
+               << "; }\n";
+        }
+    }
+    // The epilogue: input `acc_input` is the GEMM's value, the others are read
+    // at flat output index i by their access class.
+    os << "struct McEpilogue\n{\n";
+    for (std::size_t k = 0; k < num_inputs; ++k) os << "\tconst float* __restrict__ in" << k << ";\n";
+    os << "\t__device__ __forceinline__ float operator()(float v, unsigned i) const\n\t{\n\t\treturn mc_program(";
+    for (std::size_t k = 0; k < num_inputs; ++k) {
+        if (k) os << ", ";
+        if (k == acc_input) {
+            os << "v";
+            continue;
+        }
+        const Access a = classify_access(input_shapes[k], out_shape);
+        switch (a.kind) {
+            case Access::Kind::Scalar: os << "in" << k << "[0]"; break;
+            case Access::Kind::Contiguous: os << "in" << k << "[i]"; break;
+            case Access::Kind::Periodic: os << "in" << k << "[i % " << u32(a.period) << "]"; break;
+            case Access::Kind::General: os << "in" << k << "[mc_general_" << k << "(i)]"; break;
+        }
+    }
+    os << ");\n\t}\n};\n\n";
+    os << "extern \"C\" __global__ void __launch_bounds__(256, 2)\n" << kGemmEpilogueKernelName
+       << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
+          "int k_split, float* __restrict__ partial, McEpilogue epi)\n{\n"
+       << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false")
+       << ">(a, b, c, m, n, k, k_split, partial, epi);\n}\n\n";
+    // Split K: the partial sums added in split order, then the epilogue.
+    os << "extern \"C\" __global__ void __launch_bounds__(256)\n" << kSumSplitsEpilogueKernelName
+       << "(const float* __restrict__ partial, float* __restrict__ c, unsigned count, int splits, McEpilogue epi)\n{\n"
+       << "\tfor (unsigned i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {\n"
+       << "\t\tfloat s = partial[i];\n"
+       << "\t\tfor (int z = 1; z < splits; ++z) s += partial[(unsigned long long)z * count + i];\n"
+       << "\t\tc[i] = epi(s, i);\n\t}\n}\n";
+    return {os.str()};
 }
 
 CodegenOptions codegen_options(const HipOptions& options) {
@@ -170,25 +249,7 @@ ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const
     os << "typedef float mc_f32x4 __attribute__((ext_vector_type(4)));\n\n";
     if (uses_op(program, OpKind::Tanh)) os << kTanhSource;
 
-    // The program: one argument per fused input (its element, or its scalar).
-    os << "__device__ __forceinline__ float mc_program(";
-    for (std::size_t k = 0; k < num_inputs; ++k) os << (k ? ", " : "") << "float x" << k;
-    if (num_inputs == 0) os << "void";
-    os << ")\n{\n";
-    for (std::size_t r = 0; r < program.instrs.size(); ++r) {
-        const FusedInstr& ins = program.instrs[r];
-        os << "\tconst float r" << r << " = ";
-        switch (ins.kind) {
-            case FusedInstr::Kind::Load: os << "x" << ins.a; break;
-            case FusedInstr::Kind::Immediate: os << exact_float(ins.immediate); break;
-            case FusedInstr::Kind::Unary: os << op_text(ins.op, "r" + std::to_string(ins.a), ""); break;
-            case FusedInstr::Kind::Binary:
-                os << op_text(ins.op, "r" + std::to_string(ins.a), "r" + std::to_string(ins.b));
-                break;
-        }
-        os << ";\n";
-    }
-    os << "\treturn r" << program.instrs.size() - 1 << ";\n}\n\n";
+    os << program_function(program, num_inputs);
 
     // Loads and stores.
     const std::string ld_open = options.nontemporal_loads ? "__builtin_nontemporal_load(&" : "(";

@@ -63,6 +63,26 @@ Access classify_access(const Shape& in, const Shape& out);
 ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const std::vector<Shape>& input_shapes,
                                               const Shape& out_shape, const CodegenOptions& options = {});
 
+inline constexpr const char* kGemmEpilogueKernelName = "mc_gemm_epilogue";
+inline constexpr const char* kSumSplitsEpilogueKernelName = "mc_sum_splits_epilogue";
+
+struct GemmEpilogueKernel {
+    std::string source;  // defines kGemmEpilogueKernelName and kSumSplitsEpilogueKernelName
+};
+
+// An FP32 GEMM (the matrix-core body in `gemm_body_source`, 128x128 tiles,
+// 256 lanes, grid (N/128, M/128, splits)) whose store applies `program`, the
+// fused elementwise group that consumes the GEMM's result: the program's
+// input `acc_input` is the accumulated value; every other input is read at
+// the flat output index by its access class against `out_shape`. Kernel
+// arguments: (a, b, c, m, n, k, k_split, partial, epi) and, for split K,
+// (partial, c, count, splits, epi), where epi holds one float pointer per
+// program input (that of `acc_input` unused). `vectorized_operands`: A and B
+// rows allow 16-byte loads (k and n multiples of 4, 16-byte aligned).
+GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
+                                                 const std::vector<Shape>& input_shapes, const Shape& out_shape,
+                                                 bool vectorized_operands, const char* gemm_body_source);
+
 // The generator options a compiled graph uses.
 CodegenOptions codegen_options(const HipOptions& options);
 

@@ -17,6 +17,7 @@
 #include "kernel_compiler.hpp"
 #include "matmul.h"
 #include "matmul_policy.hpp"
+#include "rtc_sources.hpp"
 #include "minicompiler/runtime/memory_plan.hpp"
 
 #include <algorithm>
@@ -50,8 +51,12 @@ bool is_tensor_core(MatmulKernel k) {
 std::string arch_base(const std::string& arch) { return arch.substr(0, arch.find(':')); }
 
 struct Launch {
-    enum class Kind { Elementwise, Matmul } kind = Kind::Elementwise;
+    // FusedMatmul: an FP32 matrix-core GEMM whose store applies the fused
+    // elementwise group `epilogue_node` (compiled at run time), writing that
+    // group's output; with split K the epilogue runs in the split sum.
+    enum class Kind { Elementwise, Matmul, FusedMatmul } kind = Kind::Elementwise;
     NodeId node = kNoNode;
+    NodeId epilogue_node = kNoNode;
     // Elementwise: generated kernel, arguments out, in0.., count.
     void* function = nullptr;
     unsigned grid = 0;
@@ -63,7 +68,29 @@ struct Launch {
     int splits = 1;
     float* workspace = nullptr;
     int m = 0, n = 0, k = 0;
+    // FusedMatmul: generated kernels and their stable arguments.
+    void* sum_function = nullptr;
+    unsigned grid_x = 0, grid_y = 0, grid_z = 0, sum_grid = 0;
+    int k_split = 0;
+    const void* a_ptr = nullptr;
+    const void* b_ptr = nullptr;
+    void* c_ptr = nullptr;
+    void* partial = nullptr;
+    std::vector<const void*> epilogue_inputs;  // the McEpilogue argument: one pointer per program input
+    std::vector<void*> sum_params;
 };
+
+// K per split and number of splits as the FP32 matrix-core kernels lay them
+// out (whole 32-wide K tiles per split).
+void split_layout(int k, int splits, int* k_split, int* depth) {
+    if (splits <= 1) {
+        *k_split = std::max(k, 1);
+    } else {
+        const int per = (k + splits - 1) / splits;
+        *k_split = (per + 31) / 32 * 32;
+    }
+    *depth = std::max(1, (k + *k_split - 1) / *k_split);
+}
 
 class HipExecutableImpl final : public HipExecutable {
 public:
@@ -105,15 +132,22 @@ public:
 
         // Launches (matmul workspaces take arena space too).
         std::vector<std::size_t> workspace_offset;
+        std::vector<bool> fused_away(n, false);
         for (std::size_t i = 0; i < n; ++i) {
             const auto id = static_cast<NodeId>(i);
             const Node& node = graph_.node(id);
-            if (!is_compute(node.op)) continue;
+            if (!is_compute(node.op) || fused_away[i]) continue;
             Launch l;
             l.node = id;
             if (node.op == OpKind::MatMul) {
                 Status st = plan_matmul(node, &l);
                 if (!st.ok()) return st;
+                const NodeId f = epilogue_for(id, l);
+                if (f != kNoNode) {
+                    l.kind = Launch::Kind::FusedMatmul;
+                    l.epilogue_node = f;
+                    fused_away[static_cast<std::size_t>(f)] = true;
+                }
                 const std::size_t ws = matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
                 workspace_offset.push_back(ws ? top : SIZE_MAX);
                 if (ws) top += align_up(ws);
@@ -284,20 +318,33 @@ public:
         std::vector<std::string> names;
         for (const Launch& l : launches_) {
             const Node& node = graph_.node(l.node);
-            if (l.kind == Launch::Kind::Matmul) {
-                names.push_back(std::string("matmul ") + matmul_kernel_name(l.matmul) + " " + std::to_string(l.m) +
-                                "x" + std::to_string(l.n) + "x" + std::to_string(l.k) +
-                                (l.splits > 1 ? " splits=" + std::to_string(l.splits) : ""));
+            if (l.kind == Launch::Kind::Matmul || l.kind == Launch::Kind::FusedMatmul) {
+                std::string name = std::string("matmul ") + matmul_kernel_name(l.matmul) + " " + std::to_string(l.m) +
+                                   "x" + std::to_string(l.n) + "x" + std::to_string(l.k) +
+                                   (l.splits > 1 ? " splits=" + std::to_string(l.splits) : "");
+                if (l.kind == Launch::Kind::FusedMatmul) {
+                    const Node& f = graph_.node(l.epilogue_node);
+                    name += " + fused " + f.name + " " + to_string(f.type);
+                }
+                names.push_back(name);
             } else {
                 names.push_back(std::string(op_name(node.op)) + " " + node.name + " " + to_string(node.type));
             }
         }
         return names;
     }
+    std::vector<std::vector<NodeId>> launch_nodes() const override {
+        std::vector<std::vector<NodeId>> out;
+        for (const Launch& l : launches_) {
+            out.push_back({l.node});
+            if (l.kind == Launch::Kind::FusedMatmul) out.back().push_back(l.epilogue_node);
+        }
+        return out;
+    }
     std::vector<MatmulKernel> matmul_kernels() const override {
         std::vector<MatmulKernel> ks;
         for (const Launch& l : launches_) {
-            if (l.kind == Launch::Kind::Matmul) ks.push_back(l.matmul);
+            if (l.kind == Launch::Kind::Matmul || l.kind == Launch::Kind::FusedMatmul) ks.push_back(l.matmul);
         }
         return ks;
     }
@@ -309,6 +356,15 @@ private:
         if (l.kind == Launch::Kind::Elementwise) {
             const int rc = mchip_module_launch(l.function, l.grid, kElementwiseBlock, 0, s, l.params.data());
             return rc == 0 ? Status() : hip_status(rc, "hipModuleLaunchKernel");
+        }
+        if (l.kind == Launch::Kind::FusedMatmul) {
+            int rc = mchip_module_launch3(l.function, l.grid_x, l.grid_y, l.grid_z, 256, 0, s, l.params.data());
+            if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
+            if (l.grid_z > 1) {
+                rc = mchip_module_launch(l.sum_function, l.sum_grid, 256, 0, s, l.sum_params.data());
+                if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_sum_splits_epilogue)");
+            }
+            return Status();
         }
         const int rc = mchip_launch_matmul(static_cast<int>(l.matmul), static_cast<const float*>(value_ptr(a_of(l))),
                                            static_cast<const float*>(value_ptr(b_of(l))),
@@ -345,6 +401,54 @@ private:
         return Status();
     }
 
+    // The fused elementwise group this matmul's store can apply, or kNoNode.
+    // Only when it is safe to run the group at the matmul's place: the group
+    // is the next compute node, reads the product element for element (same
+    // element count) and is its only reader, the product is not a graph
+    // output, and the group's output buffer is none of the buffers the fused
+    // kernel reads (the memory plan may hand a buffer freed by the matmul's
+    // operands to the group's output).
+    NodeId epilogue_for(NodeId m, const Launch& l) const {
+        if (!options_.fuse_epilogue) return kNoNode;
+        if (l.matmul != MatmulKernel::Vectorized && l.matmul != MatmulKernel::DoubleBuffered &&
+            l.matmul != MatmulKernel::SplitK) {
+            return kNoNode;
+        }
+        for (NodeId o : graph_.outputs()) {
+            if (o == m) return kNoNode;
+        }
+        NodeId f = kNoNode;
+        for (std::size_t j = static_cast<std::size_t>(m) + 1; j < graph_.num_nodes(); ++j) {
+            if (is_compute(graph_.node(static_cast<NodeId>(j)).op)) {
+                f = static_cast<NodeId>(j);
+                break;
+            }
+        }
+        if (f == kNoNode) return kNoNode;
+        const Node& fn = graph_.node(f);
+        if (fn.op != OpKind::FusedElementwise || fn.type.num_elements() != graph_.node(m).type.num_elements()) {
+            return kNoNode;
+        }
+        std::size_t readers = 0;
+        for (std::size_t j = 0; j < graph_.num_nodes(); ++j) {
+            for (NodeId in : graph_.node(static_cast<NodeId>(j)).inputs) readers += in == m ? 1 : 0;
+        }
+        if (readers != 1) return kNoNode;
+        const std::int32_t out_buffer = plan_.buffer_of[static_cast<std::size_t>(f)];
+        auto shares_output_buffer = [&](NodeId id) {
+            const Node& node = graph_.node(id);
+            if (node.op == OpKind::Input || node.op == OpKind::Constant) return false;
+            return plan_.buffer_of[static_cast<std::size_t>(id)] == out_buffer;
+        };
+        for (NodeId in : graph_.node(m).inputs) {
+            if (shares_output_buffer(in)) return kNoNode;
+        }
+        for (NodeId in : fn.inputs) {
+            if (in != m && shares_output_buffer(in)) return kNoNode;
+        }
+        return f;
+    }
+
     // Generates every elementwise kernel and compiles them concurrently.
     Status build_elementwise() {
         struct Job {
@@ -354,6 +458,22 @@ private:
         std::vector<Job> jobs;
         const CodegenOptions cg = codegen_options(options_);
         for (std::size_t j = 0; j < launches_.size(); ++j) {
+            if (launches_[j].kind == Launch::Kind::FusedMatmul) {
+                const Launch& l = launches_[j];
+                const Node& f = graph_.node(l.epilogue_node);
+                std::vector<Shape> shapes;
+                std::size_t acc = 0;
+                for (std::size_t k = 0; k < f.inputs.size(); ++k) {
+                    shapes.push_back(graph_.node(f.inputs[k]).type.shape);
+                    if (f.inputs[k] == l.node) acc = k;
+                }
+                ElementwiseKernel k;
+                k.source = generate_gemm_epilogue_kernel(*f.fused, acc, shapes, f.type.shape, l.n % 4 == 0 && l.k % 4 == 0,
+                                                         kGemmF32MfmaSource)
+                               .source;
+                jobs.push_back({j, std::move(k)});
+                continue;
+            }
             if (launches_[j].kind != Launch::Kind::Elementwise) continue;
             const Node& node = graph_.node(launches_[j].node);
             const FusedProgram program =
@@ -374,7 +494,10 @@ private:
             pool.emplace_back([&]() {
                 mchip_set_device(dev);  // per thread
                 for (std::size_t j = next++; j < jobs.size(); j = next++) {
-                    built[j] = KernelCompiler::instance().get(jobs[j].kernel.source, kElementwiseKernelName, arch, dev, &ms[j]);
+                    const bool gemm = launches_[jobs[j].launch].kind == Launch::Kind::FusedMatmul;
+                    built[j] = KernelCompiler::instance().get(jobs[j].kernel.source,
+                                                              gemm ? kGemmEpilogueKernelName : kElementwiseKernelName,
+                                                              arch, dev, &ms[j]);
                 }
             });
         }
@@ -385,6 +508,24 @@ private:
             const ElementwiseKernel& kern = jobs[j].kernel;
             jit_ms_ += ms[j];
             sources_.push_back(kern.source);
+            if (l.kind == Launch::Kind::FusedMatmul) {
+                l.function = built[j]->function;
+                Result<CompiledKernel> sum = KernelCompiler::instance().get(kern.source, kSumSplitsEpilogueKernelName,
+                                                                            arch, dev, nullptr);
+                if (!sum.ok()) return sum.error();
+                l.sum_function = sum->function;
+                int depth = 1;
+                split_layout(l.k, l.splits, &l.k_split, &depth);
+                l.grid_x = static_cast<unsigned>((l.n + 127) / 128);
+                l.grid_y = static_cast<unsigned>((l.m + 127) / 128);
+                l.grid_z = static_cast<unsigned>(depth);
+                l.count = static_cast<unsigned>(static_cast<std::size_t>(l.m) * l.n);
+                l.sum_grid = static_cast<unsigned>(std::max<std::size_t>(
+                    1, std::min<std::size_t>((static_cast<std::size_t>(l.count) + 255) / 256, 8192)));
+                l.partial = depth > 1 ? l.workspace : nullptr;
+                l.epilogue_inputs.assign(graph_.node(l.epilogue_node).inputs.size(), nullptr);
+                continue;
+            }
             const std::size_t numel = graph_.node(l.node).type.num_elements();
             l.function = built[j]->function;
             l.count = static_cast<unsigned>(kern.vectorized ? numel / 4 : numel);
@@ -401,6 +542,12 @@ private:
         }
         // Stable argument addresses: the launch list no longer changes.
         for (Launch& l : launches_) {
+            if (l.kind == Launch::Kind::FusedMatmul) {
+                l.params = {&l.a_ptr, &l.b_ptr, &l.c_ptr, &l.m, &l.n, &l.k, &l.k_split, &l.partial,
+                            l.epilogue_inputs.data()};
+                l.sum_params = {&l.partial, &l.c_ptr, &l.count, &l.grid_z, l.epilogue_inputs.data()};
+                continue;
+            }
             if (l.kind != Launch::Kind::Elementwise) continue;
             for (void*& p : l.ptrs) l.params.push_back(&p);
             l.params.push_back(&l.count);
@@ -411,6 +558,16 @@ private:
     void refresh_pointers() {
         if (output_bound_.size() != graph_.outputs().size()) output_bound_.assign(graph_.outputs().size(), nullptr);
         for (Launch& l : launches_) {
+            if (l.kind == Launch::Kind::FusedMatmul) {
+                l.a_ptr = value_ptr(a_of(l));
+                l.b_ptr = value_ptr(b_of(l));
+                l.c_ptr = value_ptr(l.epilogue_node);
+                const Node& f = graph_.node(l.epilogue_node);
+                for (std::size_t k = 0; k < f.inputs.size(); ++k) {
+                    l.epilogue_inputs[k] = f.inputs[k] == l.node ? nullptr : value_ptr(f.inputs[k]);
+                }
+                continue;
+            }
             if (l.kind != Launch::Kind::Elementwise) continue;
             const Node& node = graph_.node(l.node);
             l.ptrs[0] = value_ptr(l.node);

@@ -127,6 +127,11 @@ int mchip_module_launch(void* function, unsigned grid, unsigned block, unsigned 
     return hipModuleLaunchKernel(static_cast<hipFunction_t>(function), grid, 1, 1, block, 1, 1, shared_bytes,
                                  static_cast<hipStream_t>(stream), params, nullptr);
 }
+int mchip_module_launch3(void* function, unsigned grid_x, unsigned grid_y, unsigned grid_z, unsigned block,
+                         unsigned shared_bytes, void* stream, void** params) {
+    return hipModuleLaunchKernel(static_cast<hipFunction_t>(function), grid_x, grid_y, grid_z, block, 1, 1,
+                                 shared_bytes, static_cast<hipStream_t>(stream), params, nullptr);
+}
 int mchip_occupancy(int* blocks_per_cu, void* function, int block, size_t shared_bytes) {
     return hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, static_cast<hipFunction_t>(function),
                                                               block, shared_bytes);

@@ -70,6 +70,8 @@ int mchip_module_unload(void* module);
 int mchip_module_function(void** function, void* module, const char* name);
 int mchip_module_launch(void* function, unsigned grid, unsigned block, unsigned shared_bytes, void* stream,
                         void** params);
+int mchip_module_launch3(void* function, unsigned grid_x, unsigned grid_y, unsigned grid_z, unsigned block,
+                         unsigned shared_bytes, void* stream, void** params);
 int mchip_occupancy(int* blocks_per_cu, void* function, int block, size_t shared_bytes);
 
 #ifdef __cplusplus

@@ -104,26 +104,37 @@ Result<std::string> KernelCompiler::compile_code_object(const std::string& sourc
 Result<CompiledKernel> KernelCompiler::get(const std::string& source, const char* name, const std::string& arch,
                                            int device, double* compile_ms) {
     if (compile_ms) *compile_ms = 0.0;
-    const std::string key = std::to_string(device) + '\n' + cache_key(arch, source) + '\n' + name;
+    const std::string module_key = std::to_string(device) + '\n' + cache_key(arch, source);
+    const std::string key = module_key + '\n' + name;
+    void* module = nullptr;
     {
         std::lock_guard<std::mutex> lock(mutex_);
         const auto it = loaded_.find(key);
         if (it != loaded_.end()) return it->second;
+        const auto m = modules_.find(module_key);
+        if (m != modules_.end()) module = m->second;
     }
-    // Compile outside the lock so executables can build kernels concurrently.
-    Result<std::string> code = compile_code_object(source, arch, compile_ms);
-    if (!code.ok()) return code.error();
+    if (module == nullptr) {
+        // Compile outside the lock so executables can build kernels concurrently.
+        Result<std::string> code = compile_code_object(source, arch, compile_ms);
+        if (!code.ok()) return code.error();
+        std::lock_guard<std::mutex> lock(mutex_);
+        const auto m = modules_.find(module_key);
+        if (m != modules_.end()) {
+            module = m->second;
+        } else {
+            const int rc = mchip_module_load(&module, code->data());
+            if (rc != 0) return Error{std::string("hipModuleLoadData: ") + mchip_error_string(rc)};
+            modules_.emplace(module_key, module);
+        }
+    }
     std::lock_guard<std::mutex> lock(mutex_);
     const auto it = loaded_.find(key);
     if (it != loaded_.end()) return it->second;
     CompiledKernel k;
-    int rc = mchip_module_load(&k.module, code->data());
-    if (rc != 0) return Error{std::string("hipModuleLoadData: ") + mchip_error_string(rc)};
-    rc = mchip_module_function(&k.function, k.module, name);
-    if (rc != 0) {
-        mchip_module_unload(k.module);
-        return Error{std::string("hipModuleGetFunction(") + name + "): " + mchip_error_string(rc)};
-    }
+    k.module = module;
+    const int rc = mchip_module_function(&k.function, module, name);
+    if (rc != 0) return Error{std::string("hipModuleGetFunction(") + name + "): " + mchip_error_string(rc)};
     loaded_.emplace(key, k);
     return k;
 }

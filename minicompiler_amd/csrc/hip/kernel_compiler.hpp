@@ -42,7 +42,8 @@ public:
 
 private:
     std::mutex mutex_;
-    std::map<std::string, CompiledKernel> loaded_;
+    std::map<std::string, CompiledKernel> loaded_;   // (device, arch, options, source, name) -> function
+    std::map<std::string, void*> modules_;           // (device, arch, options, source) -> module
 };
 
 }  // namespace minicompiler::hip

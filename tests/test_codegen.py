@@ -127,3 +127,28 @@ def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, ou
 def test_a_bad_generated_source_returns_the_hiprtc_log(mc):
     ok, log = mc.compile_kernel_source('extern "C" __global__ void mc_elementwise() { undefined_thing(); }')
     assert not ok and "undefined_thing" in log and "hipRTC could not compile" in log
+
+
+@pytest.mark.parametrize("text,acc,shapes,out,vec", [
+    # bias + GELU on a GEMM result (the MLP's first group), 16-byte operand loads
+    (GELU.replace("load in0", "load in0"), 0, None, None, True),
+    # bias + residual, the product as the second input; scalar operand loads
+    ("r0 = load in0\nr1 = load in1\nr2 = add r0, r1\nr3 = load in2\nr4 = add r2, r3\n", 1,
+     [(512,), (64, 512), (64, 512)], (64, 512), False),
+    # a general broadcast and a scalar next to the product
+    ("r0 = load in0\nr1 = load in1\nr2 = mul r0, r1\nr3 = load in2\nr4 = sub r2, r3\n", 0,
+     [(5, 8), (5, 1), ()], (5, 8), True),
+])
+def test_gemm_epilogue_kernels_compile_for_gfx950_without_a_gpu(mc, text, acc, shapes, out, vec):
+    if shapes is None:
+        shapes, out = [(64, 128)], (64, 128)
+        text = "r0 = load in0\nr1 = imm 0x3f000000\nr2 = mul r0, r1\nr3 = tanh r2\n"
+    src = mc.generate_gemm_epilogue_kernel(text, acc, shapes, out, vec)
+    assert "mc_gemm_f32_mfma<true, " + ("true" if vec else "false") + ">" in src
+    assert "extern \"C\" __global__ void __launch_bounds__(256, 2)\nmc_gemm_epilogue(" in src
+    assert "mc_sum_splits_epilogue(" in src
+    # The product enters the program as the accumulated value, the others by access class.
+    call = src[src.index("return mc_program("):].split("\n")[0]
+    assert call.split("(", 1)[1].split(",")[acc].strip(" );") == "v"
+    ok, log = mc.compile_kernel_source(src, "gfx950")
+    assert ok, log

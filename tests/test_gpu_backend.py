@@ -317,3 +317,57 @@ def test_the_pre_cast_matrix_core_path_matches_the_staging_path(device, mc, orac
             assert np.array_equal((bits << 16).view(np.float32), rnd)
         else:
             assert np.array_equal(bits.astype(np.uint16).view(np.float16).astype(np.float32), rnd)
+
+
+MLP = ("mlp_gelu", {"B": 256}), ("mlp_gelu", {"B": 1024})
+
+
+@pytest.mark.parametrize("name,dims", MLP + (("matmul_bias_gelu", {"M": 300, "K": 256, "N": 520}),
+                                             ("matmul_bias_relu", None)))
+@pytest.mark.parametrize("matmul", ["auto", "double_buffered", "split_k"])
+def test_fused_gemm_epilogues_equal_the_separate_kernels_bit_for_bit(device, mc, oracle, name, dims, matmul):
+    # The GEMM's store applies the consuming elementwise group: the same fp32
+    # accumulation and the same per-op rounding, so identical bits.
+    fused = mc.Compiled(path=mc.graph_path(name), dims=dims, options={"matmul": matmul})
+    apart = mc.Compiled(path=mc.graph_path(name), dims=dims, options={"matmul": matmul, "epilogue": 0})
+    assert any(len(ids) > 1 for ids in fused.launch_nodes), fused.launch_names
+    assert all(len(ids) == 1 for ids in apart.launch_nodes)
+    assert fused.kernel_launches < apart.kernel_launches
+    inputs = uniform_inputs(oracle, fused.input_sizes, 1)
+    a, b = fused.run(inputs), apart.run(inputs)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), (name, matmul)
+    cpu = oracle.evaluate_compiled(fused, inputs)
+    assert_close(a[0], cpu[0], 1e-4, 1e-4 * max(1.0, max_abs(cpu[0])), f"{name} fused vs CPU")
+
+
+def test_epilogue_fusion_is_refused_when_the_group_is_not_next_or_reads_the_product_twice(device, mc, oracle):
+    # A compute node between the matmul and its consumer: not fused (the
+    # consumer's other input is computed after the matmul).
+    text = """input a : f32[64, 32]
+input w : f32[32, 48]
+input z : f32[64, 48]
+h = matmul a, w
+e = exp z
+s = add h, e
+t = mul s, s
+output t
+"""
+    c = mc.Compiled(text)
+    inputs = uniform_inputs(oracle, c.input_sizes, 3)
+    gpu = c.run(inputs)
+    cpu = oracle.evaluate_compiled(c, inputs)
+    assert_close(gpu[0], cpu[0], 1e-4, 1e-4 * max(1.0, max_abs(cpu[0])))
+    graph = c.graph()
+    matmul_ids = [n["id"] for n in graph["nodes"] if n["op_name"] == "matmul"]
+    for ids in c.launch_nodes:
+        if ids[0] in matmul_ids:
+            # fused only if the consumer is the very next compute node
+            assert len(ids) == 1 or ids[1] == ids[0] + 1
+    # The product also a graph output: never fused.
+    text2 = "input a : f32[64, 32]\ninput w : f32[32, 48]\nh = matmul a, w\ny = relu h\noutput h\noutput y\n"
+    c2 = mc.Compiled(text2)
+    assert all(len(ids) == 1 for ids in c2.launch_nodes)
+    inputs2 = uniform_inputs(oracle, c2.input_sizes, 4)
+    for g, r in zip(c2.run(inputs2), oracle.evaluate_compiled(c2, inputs2)):
+        assert_close(g, r, 1e-4, 1e-4 * max(1.0, max_abs(r)))

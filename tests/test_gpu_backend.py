@@ -234,12 +234,15 @@ def test_random_graphs_match_the_cpu_oracle(device, mc, oracle):
 
 
 def test_fusion_cuts_kernel_launches(device, mc):
-    # tests/test_cuda_backend.cpp:421-433.
+    # tests/test_cuda_backend.cpp:439-451, from tests/golden/reference_known_answers.json.
+    import json
+    from pathlib import Path
+    case = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())["launch_counts"]
+
     def launches(passes):
-        return mc.Compiled(path=mc.graph_path("gelu_chain"), dims={"M": 8, "N": 128}, passes=passes).kernel_launches
-    assert launches("none") == 11
-    assert launches("dne,fold,dne") == 9
-    assert launches("default") == 1
+        return mc.Compiled(path=mc.graph_path(case["graph"]), dims=case["dims"], passes=passes).kernel_launches
+    for passes in ("none", "dne,fold,dne", "default"):
+        assert launches(passes) == case[passes], passes
 
 
 def test_reuses_intermediate_buffers_on_the_device(device, mc):

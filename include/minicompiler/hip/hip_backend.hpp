@@ -73,6 +73,14 @@ struct HipOptions {
     // the store of an FP32 matrix-core GEMM (one kernel instead of two), when
     // the memory plan makes that safe.
     bool fuse_epilogue = true;
+    // Tensor-core matmuls (bf16 / fp16) in a compiled graph: round the fp32
+    // operands to 16 bits into workspace first (constants once, at compile
+    // time), then run the 256x256-tile kernel on them, when the shape allows
+    // (K a multiple of 64, N a multiple of 8). The rounding and the
+    // accumulation order are those of the staging kernel with K unsplit, so
+    // results match that kernel bit for bit. Off: the staging kernel rounds
+    // while it stages (and splits K where SplitK would).
+    bool convert_tensor_core_operands = true;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).

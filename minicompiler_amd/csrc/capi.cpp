@@ -118,6 +118,8 @@ Result<hip::HipOptions> parse_options(const char* spec) {
                 return Error{"option " + key + " out of range: " + value};
             }
             (key == "ew_items" ? o.elementwise_items : o.elementwise_blocks_per_cu) = static_cast<unsigned>(v.value());
+        } else if (key == "tc_convert") {
+            o.convert_tensor_core_operands = value != "0" && value != "false";
         } else if (key == "epilogue") {
             o.fuse_epilogue = value != "0" && value != "false";
         } else if (key == "ew_nt_loads") {
@@ -126,7 +128,8 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             o.nontemporal_stores = value != "0" && value != "false";
         } else {
             return Error{"unknown option '" + key +
-                         "' (matmul, vectorize, device, epilogue, ew_items, ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
+                         "' (matmul, vectorize, device, epilogue, tc_convert, ew_items, ew_nt_loads, ew_nt_stores, "
+                         "ew_blocks_per_cu)"};
         }
     }
     return o;

@@ -152,10 +152,12 @@ Access classify_access(const Shape& in, const Shape& out) {
 
 GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
                                                  const std::vector<Shape>& input_shapes, const Shape& out_shape,
-                                                 bool vectorized_operands, const char* gemm_body_source) {
+                                                 bool vectorized_operands, const char* gemm_body_source,
+                                                 GemmBody body) {
     const std::size_t num_inputs = input_shapes.size();
     std::ostringstream os;
-    os << "// minicompiler-hip FP32 GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
+    os << "// minicompiler-hip " << (body == GemmBody::F32Mfma ? "FP32" : body == GemmBody::Bf16Fast ? "bf16" : "fp16")
+       << " GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
        << to_string(out_shape) << ".\n";
     os << gemm_body_source << "\n";
     if (uses_op(program, OpKind::Tanh)) os << kTanhSource;
@@ -189,6 +191,14 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         }
     }
     os << ");\n\t}\n};\n\n";
+    if (body != GemmBody::F32Mfma) {
+        os << "extern \"C\" __global__ void __launch_bounds__(512, 1)\n" << kGemmEpilogueKernelName
+           << "(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b, float* __restrict__ c, "
+              "int m, int n, int k, McEpilogue epi)\n{\n"
+           << "\tmc_gemm16_fast<" << (body == GemmBody::Bf16Fast ? "true" : "false")
+           << ">(a, b, c, m, n, k, epi);\n}\n";
+        return {os.str()};
+    }
     os << "extern \"C\" __global__ void __launch_bounds__(256, 2)\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
           "int k_split, float* __restrict__ partial, McEpilogue epi)\n{\n"

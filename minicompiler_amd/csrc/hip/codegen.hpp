@@ -67,21 +67,31 @@ inline constexpr const char* kGemmEpilogueKernelName = "mc_gemm_epilogue";
 inline constexpr const char* kSumSplitsEpilogueKernelName = "mc_sum_splits_epilogue";
 
 struct GemmEpilogueKernel {
-    std::string source;  // defines kGemmEpilogueKernelName and kSumSplitsEpilogueKernelName
+    std::string source;  // defines kGemmEpilogueKernelName (and, FP32, kSumSplitsEpilogueKernelName)
 };
 
-// An FP32 GEMM (the matrix-core body in `gemm_body_source`, 128x128 tiles,
-// 256 lanes, grid (N/128, M/128, splits)) whose store applies `program`, the
+// Which GEMM body the epilogue kernel wraps.
+enum class GemmBody {
+    F32Mfma,   // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K
+    Bf16Fast,  // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
+    F16Fast,   // fp16 operands, likewise
+};
+
+// A GEMM (the matrix-core body in `gemm_body_source`, of kind `body`) whose
+// store applies `program`, the
 // fused elementwise group that consumes the GEMM's result: the program's
 // input `acc_input` is the accumulated value; every other input is read at
 // the flat output index by its access class against `out_shape`. Kernel
-// arguments: (a, b, c, m, n, k, k_split, partial, epi) and, for split K,
-// (partial, c, count, splits, epi), where epi holds one float pointer per
-// program input (that of `acc_input` unused). `vectorized_operands`: A and B
+// arguments, FP32 body (grid (N/128, M/128, splits), 256 lanes):
+// (a, b, c, m, n, k, k_split, partial, epi) and, for split K, (partial, c,
+// count, splits, epi); 16-bit bodies (one block of 512 lanes per 256x256
+// tile): (a, b, c, m, n, k, epi). epi holds one float pointer per program
+// input (that of `acc_input` unused). `vectorized_operands` (FP32): A and B
 // rows allow 16-byte loads (k and n multiples of 4, 16-byte aligned).
 GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
                                                  const std::vector<Shape>& input_shapes, const Shape& out_shape,
-                                                 bool vectorized_operands, const char* gemm_body_source);
+                                                 bool vectorized_operands, const char* gemm_body_source,
+                                                 GemmBody body = GemmBody::F32Mfma);
 
 // The generator options a compiled graph uses.
 CodegenOptions codegen_options(const HipOptions& options);

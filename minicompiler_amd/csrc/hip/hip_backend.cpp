@@ -78,6 +78,14 @@ struct Launch {
     void* partial = nullptr;
     std::vector<const void*> epilogue_inputs;  // the McEpilogue argument: one pointer per program input
     std::vector<void*> sum_params;
+    // Tensor-core matmul on fp32 operands rounded to 16 bits in the launch's
+    // workspace (a16, b16) first: per run, or once at compile time for a
+    // constant operand.
+    bool lowp = false;
+    int dtype = 0;
+    void* a16 = nullptr;
+    void* b16 = nullptr;
+    bool convert_a = false, convert_b = false;
 };
 
 // K per split and number of splits as the FP32 matrix-core kernels lay them
@@ -148,7 +156,9 @@ public:
                     l.epilogue_node = f;
                     fused_away[static_cast<std::size_t>(f)] = true;
                 }
-                const std::size_t ws = matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
+                const std::size_t ws =
+                    l.lowp ? align_up(static_cast<std::size_t>(l.m) * l.k * 2) + align_up(static_cast<std::size_t>(l.k) * l.n * 2)
+                           : matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
                 workspace_offset.push_back(ws ? top : SIZE_MAX);
                 if (ws) top += align_up(ws);
             } else {
@@ -161,13 +171,32 @@ public:
         MCHIP_TRY(mchip_malloc(&arena_, arena_bytes_));
         auto* base = static_cast<char*>(arena_);
         for (std::size_t j = 0; j < launches_.size(); ++j) {
-            if (workspace_offset[j] != SIZE_MAX) launches_[j].workspace = reinterpret_cast<float*>(base + workspace_offset[j]);
+            if (workspace_offset[j] == SIZE_MAX) continue;
+            Launch& l = launches_[j];
+            if (l.lowp) {
+                l.a16 = base + workspace_offset[j];
+                l.b16 = base + workspace_offset[j] + align_up(static_cast<std::size_t>(l.m) * l.k * 2);
+            } else {
+                l.workspace = reinterpret_cast<float*>(base + workspace_offset[j]);
+            }
         }
         // Constants are uploaded once, here.
         for (std::size_t i = 0; i < n; ++i) {
             const Node& node = graph_.node(static_cast<NodeId>(i));
             if (node.op != OpKind::Constant) continue;
             MCHIP_TRY(mchip_memcpy_htod_async(base + offset_[i], node.constant->data(), node.type.size_bytes(), stream_));
+        }
+        // Constant operands of converted tensor-core matmuls: rounded once, here.
+        for (const Launch& l : launches_) {
+            if (!l.lowp) continue;
+            if (!l.convert_a) {
+                MCHIP_TRY(mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16,
+                                            static_cast<std::size_t>(l.m) * l.k, stream_));
+            }
+            if (!l.convert_b) {
+                MCHIP_TRY(mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(b_of(l))), l.b16,
+                                            static_cast<std::size_t>(l.k) * l.n, stream_));
+            }
         }
         MCHIP_TRY(mchip_stream_synchronize(stream_));
 
@@ -357,6 +386,29 @@ private:
             const int rc = mchip_module_launch(l.function, l.grid, kElementwiseBlock, 0, s, l.params.data());
             return rc == 0 ? Status() : hip_status(rc, "hipModuleLaunchKernel");
         }
+        if (l.lowp) {
+            int rc = 0;
+            if (l.convert_a) {
+                rc = mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16,
+                                       static_cast<std::size_t>(l.m) * l.k, s);
+            }
+            if (rc == 0 && l.convert_b) {
+                rc = mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(b_of(l))), l.b16,
+                                       static_cast<std::size_t>(l.k) * l.n, s);
+            }
+            if (rc != 0) return hip_status(rc, "convert_f32");
+            if (l.kind == Launch::Kind::FusedMatmul) {
+                rc = mchip_module_launch(l.function, l.grid_x, 512, 0, s, l.params.data());
+                return rc == 0 ? Status() : hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
+            }
+            rc = mchip_launch_matmul_lowp(static_cast<int>(l.matmul), l.dtype, l.a16, l.b16,
+                                          static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, 1, nullptr);
+            if (rc != 0) {
+                return Error{std::string("launch_matmul_lowp(") + matmul_kernel_name(l.matmul) + "): " +
+                             mchip_error_string(rc)};
+            }
+            return Status();
+        }
         if (l.kind == Launch::Kind::FusedMatmul) {
             int rc = mchip_module_launch3(l.function, l.grid_x, l.grid_y, l.grid_z, 256, 0, s, l.params.data());
             if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
@@ -398,6 +450,14 @@ private:
                          "): gfx950 has bf16 and fp16 matrix instructions but no xf32 (TF32) one"};
         }
         l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
+        const bool bf16 = l->matmul == MatmulKernel::TensorCoreBf16, f16 = l->matmul == MatmulKernel::TensorCoreF16;
+        if (options_.convert_tensor_core_operands && (bf16 || f16) && l->k % 64 == 0 && l->n % 8 == 0 && l->n >= 8) {
+            l->lowp = true;
+            l->splits = 1;
+            l->dtype = bf16 ? MCHIP_DTYPE_BF16 : MCHIP_DTYPE_F16;
+            l->convert_a = graph_.node(node.inputs[0]).op != OpKind::Constant;
+            l->convert_b = graph_.node(node.inputs[1]).op != OpKind::Constant;
+        }
         return Status();
     }
 
@@ -410,7 +470,7 @@ private:
     // operands to the group's output).
     NodeId epilogue_for(NodeId m, const Launch& l) const {
         if (!options_.fuse_epilogue) return kNoNode;
-        if (l.matmul != MatmulKernel::Vectorized && l.matmul != MatmulKernel::DoubleBuffered &&
+        if (!l.lowp && l.matmul != MatmulKernel::Vectorized && l.matmul != MatmulKernel::DoubleBuffered &&
             l.matmul != MatmulKernel::SplitK) {
             return kNoNode;
         }
@@ -468,8 +528,10 @@ private:
                     if (f.inputs[k] == l.node) acc = k;
                 }
                 ElementwiseKernel k;
+                const GemmBody body = !l.lowp ? GemmBody::F32Mfma
+                                      : l.dtype == MCHIP_DTYPE_BF16 ? GemmBody::Bf16Fast : GemmBody::F16Fast;
                 k.source = generate_gemm_epilogue_kernel(*f.fused, acc, shapes, f.type.shape, l.n % 4 == 0 && l.k % 4 == 0,
-                                                         kGemmF32MfmaSource)
+                                                         l.lowp ? kGemm16FastSource : kGemmF32MfmaSource, body)
                                .source;
                 jobs.push_back({j, std::move(k)});
                 continue;
@@ -508,6 +570,13 @@ private:
             const ElementwiseKernel& kern = jobs[j].kernel;
             jit_ms_ += ms[j];
             sources_.push_back(kern.source);
+            if (l.kind == Launch::Kind::FusedMatmul && l.lowp) {
+                l.function = built[j]->function;
+                l.grid_x = static_cast<unsigned>(((l.m + 255) / 256) * ((l.n + 255) / 256));
+                l.grid_y = l.grid_z = 1;
+                l.epilogue_inputs.assign(graph_.node(l.epilogue_node).inputs.size(), nullptr);
+                continue;
+            }
             if (l.kind == Launch::Kind::FusedMatmul) {
                 l.function = built[j]->function;
                 Result<CompiledKernel> sum = KernelCompiler::instance().get(kern.source, kSumSplitsEpilogueKernelName,
@@ -542,6 +611,10 @@ private:
         }
         // Stable argument addresses: the launch list no longer changes.
         for (Launch& l : launches_) {
+            if (l.kind == Launch::Kind::FusedMatmul && l.lowp) {
+                l.params = {&l.a16, &l.b16, &l.c_ptr, &l.m, &l.n, &l.k, l.epilogue_inputs.data()};
+                continue;
+            }
             if (l.kind == Launch::Kind::FusedMatmul) {
                 l.params = {&l.a_ptr, &l.b_ptr, &l.c_ptr, &l.m, &l.n, &l.k, &l.k_split, &l.partial,
                             l.epilogue_inputs.data()};

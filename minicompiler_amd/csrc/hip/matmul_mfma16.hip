@@ -22,6 +22,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "gemm_mfma16_fast.h"
+
 #include <algorithm>
 #include <cstddef>
 #include <cstdint>
@@ -200,237 +202,14 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 
 // ---------------------------------------------------------------- fast path
 //
-// 16-bit inputs already in HBM, K a multiple of 64, N a multiple of 8, rows
-// 16-byte aligned. Block tile 256x256, 512 lanes = 8 waves in a 2x4 grid
-// (two waves per SIMD), each wave a 128x64 quadrant as 8x4 accumulators of
-// v_mfma_f32_16x16x32 (128 fp32 per lane, in AGPRs). One block per CU; the
-// two waves of a SIMD hide each other's LDS and barrier waits.
-//
-// K is walked in steps of 32 through a ring of four 32 KiB LDS stages, with
-// the two waves of each SIMD in ping-pong: waves 0-3 and waves 4-7 run the
-// same sequence one phase apart, alternating a memory phase (issue the
-// global -> LDS fetch of step t+3, read step t's operands from LDS into
-// registers) and a compute phase (step t's 32 MFMAs), so each SIMD's matrix
-// unit is fed by one wave while the other loads. Phases are separated by a
-// plain s_barrier of all 8 waves (no memory fence: a fence would also wait
-// for the fetches still in flight); a memory phase ends with a wait for this
-// wave's fetch of step t+1 and for its LDS reads.
-//
-// Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
-// 16 bytes at (LDS base + 16 l), so one wave instruction fills 1 KiB of LDS;
-// the swizzles below are applied by choosing which global chunk each lane
-// fetches. Rows and columns past the matrix edge are clamped to the last row
-// / column chunk, so every fetch is in bounds; the values they bring only
-// reach C rows or columns that are not stored.
-//
-// LDS layout of a stage (bytes):
-//   A [16 blocks of 16 rows][4 chunks of 8 k][16 rows], at 0: chunk c of
-//     row r at 1024 (r / 16) + 256 c + 16 (r % 16). A fragment read (16 rows
-//     x one chunk per 16 lanes, ds_read_b128) is then 1 KiB read linearly
-//     (lane l at 16 l), which gfx950 serves without bank conflicts; row-major
-//     rows with any chunk swizzle measured 4 conflict cycles per read. One
-//     fetch instruction still covers 16 whole rows (64 bytes each).
-//   B [32 k rows][32 chunks of 8 n], at 16 KiB: k row kr at 512 kr; logical
-//     chunk c stored at chunk c ^ 2 tb(kr), tb(kr) = (kr & 3) | ((kr >> 3) & 3) << 2,
-//     i.e. 32-byte pairs XOR tb. B stays n-contiguous and is read with
-//     ds_read_b64_tr_b16: within each 16 lanes, lane 4e + c supplies the
-//     address of 4 values (row e, columns 4c..4c+3) and lane i receives
-//     column i of rows 0..3. Two such reads give a lane the 8 consecutive k
-//     of one column that the MFMA B operand needs. The 16 rows one read
-//     instruction touches fall in distinct 32-byte bank windows.
-//
-// The MFMA is issued with the B fragment as its first operand and the A
-// fragment as its second, which yields C^T tiles: value v of lane l is
-// C[m0 + l % 16][n0 + 4 (l / 16) + v], four consecutive columns, stored as
-// one 16-byte write.
-//
-// Tiles are handed out in row-major order. The 256 blocks resident at a time
-// then cover a band of a few tile rows across all of N: A's band and all of
-// B (160 MiB at 8192^3) stay inside the 256 MiB MALL, and each XCD (block b
-// runs on XCD b % 8) holds every eighth tile column of the band. Measured
-// against grouped and XCD-remapped orders (A and B panels shared inside one
-// XCD's L2, but the XCDs spread over all of A), row-major was as fast or
-// faster at 8192^3.
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-#define MC_LDS __attribute__((address_space(3)))
-
-constexpr int kFBM = 256, kFBN = 256, kFBK = 32;
-constexpr int kFThreads = 512;
-constexpr int kFWaves = kFThreads / 64;
-constexpr int kFStages = 4;
-constexpr int kFStage = 32 * 1024;
-constexpr int kFBOffset = 16 * 1024;
-constexpr int kFRowFrags = 8;  // 16-row A fragments per wave (128 rows)
-constexpr int kFColFrags = 4;  // 16-column B fragments per wave (64 columns)
-// global_load_lds instructions per wave per step: 2 for A, 2 for B.
-constexpr int kFFetchPerStep = 4;
-
-__device__ __forceinline__ int swz_b(int kr) { return (kr & 3) | (((kr >> 3) & 3) << 2); }
-
-// Per-lane addressing, set up once per block.
-struct FastLane {
-    const unsigned short* a_src[2];  // A chunk this lane fetches per instruction (k offset 0)
-    const unsigned short* b_src[2];  // B chunk (k row offset 0)
-    std::ptrdiff_t b_step;           // elements between consecutive K steps of B
-    int a_off[kFRowFrags];           // LDS byte offsets of the A fragments
-    int b_off[2][kFColFrags];        // LDS byte offsets of the two transposed B reads
-    int wave;
-};
-
-__device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastLane& L, int fetch_k) {
-    MC_LDS unsigned char* sa = wr + L.wave * 32 * 64;
-    MC_LDS unsigned char* sb = wr + kFBOffset + L.wave * 4 * 512;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.a_src[i] + fetch_k),
-                                         reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
-    }
-    const std::ptrdiff_t bk = (fetch_k / kFBK) * L.b_step;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.b_src[i] + bk),
-                                         reinterpret_cast<MC_LDS void*>(sb + i * 1024), 16, 0, 0);
-    }
-}
-
-__device__ __forceinline__ u16x8 fast_read_a(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
-    return *reinterpret_cast<const MC_LDS u16x8*>(rd + L.a_off[f]);
-}
-
-__device__ __forceinline__ u16x8 fast_read_b(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
-    MC_LDS unsigned char* p = const_cast<MC_LDS unsigned char*>(rd);
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[0][f]));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[1][f]));
-    return __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// Memory phase: fetch step `fetch_k` into `wr` and read the operands of the
-// step held in `rd` into (av, bv). `rd` and `wr` are distinct stages;
-// declaring them __restrict__ gives the LDS reads alias scopes that keep the
-// compiler from making them wait for the fetch.
-__device__ __forceinline__ void fast_memory_phase(const MC_LDS unsigned char* __restrict__ rd,
-                                                  MC_LDS unsigned char* __restrict__ wr, const FastLane& L, int fetch_k,
-                                                  u16x8 (&av)[kFRowFrags], u16x8 (&bv)[kFColFrags]) {
-    fast_fetch(wr, L, fetch_k);
-#pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) av[f] = fast_read_a(rd, L, f);
-#pragma unroll
-    for (int f = 0; f < kFColFrags; ++f) bv[f] = fast_read_b(rd, L, f);
-}
-
-// A workgroup barrier without a memory fence; the compiler may not move
-// memory operations or MFMAs across it.
-__device__ __forceinline__ void step_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
+// The body lives in gemm_mfma16_fast.h (also compiled at run time with fused
+// epilogues); here it is instantiated with the identity epilogue.
 
 template <bool kBf16>
 __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigned short* __restrict__ a,
                                                                    const unsigned short* __restrict__ b,
                                                                    float* __restrict__ c, int m, int n, int k) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[kFStages * kFStage];
-    MC_LDS unsigned char* lds = (MC_LDS unsigned char*)(smem);  // generic -> LDS address space
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-
-    // Tile of this block (row-major).
-    const int tiles_n = (n + kFBN - 1) / kFBN;
-    const int tm = static_cast<int>(blockIdx.x) / tiles_n, tn = static_cast<int>(blockIdx.x) % tiles_n;
-    const int row0 = tm * kFBM, col0 = tn * kFBN;
-
-    FastLane L;
-    L.wave = wave;
-    // A: wave w fills the 16-row blocks 2 w and 2 w + 1, one per
-    // instruction; lane -> (row 32 w + 16 i + l % 16, chunk l / 16).
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = wave * 32 + i * 16 + (lane & 15);
-        const int gr = min(row0 + r, m - 1);
-        L.a_src[i] = a + static_cast<std::ptrdiff_t>(gr) * k + (lane >> 4) * 8;
-    }
-    // B: wave w fills k rows 4 w .. 4 w + 3, two per instruction; lane ->
-    // (k row 4 w + 2 i + l / 32, physical chunk l % 32).
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int kr = wave * 4 + i * 2 + (lane >> 5);
-        const int lc = (lane & 31) ^ (2 * swz_b(kr));
-        const int gc = min(col0 + lc * 8, n - 8);
-        L.b_src[i] = b + static_cast<std::ptrdiff_t>(kr) * n + gc;
-    }
-    L.b_step = static_cast<std::ptrdiff_t>(kFBK) * n;
-    // Wave (wm, wn) of the 2x4 grid owns rows 128 wm .., columns 64 wn ...
-    const int wr = (wave >> 2) * 128, wc = (wave & 3) * 64;
-    const int li = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) L.a_off[f] = (wr + f * 16) * 64 + lane * 16;
-    // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
-    // k row 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
-    const int te = (lane & 15) >> 2, tc = lane & 3;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int f = 0; f < kFColFrags; ++f) {
-            const int kr = 8 * g + 4 * h + te;
-            const int ncol = wc + f * 16 + 4 * tc;
-            const int chunk = (ncol >> 3) ^ (2 * swz_b(kr));
-            L.b_off[h][f] = kFBOffset + kr * 512 + (chunk << 4) + ((ncol & 4) << 1);
-        }
-
-    f32x4 acc[kFRowFrags][kFColFrags];
-#pragma unroll
-    for (int i = 0; i < kFRowFrags; ++i)
-#pragma unroll
-        for (int j = 0; j < kFColFrags; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int steps = k / kFBK;
-    auto stage = [&](int t) { return lds + (t & (kFStages - 1)) * kFStage; };
-    u16x8 av[kFRowFrags], bv[kFColFrags];
-    // Prologue: steps 0..2 landed.
-    const int pre = min(steps, kFStages - 1);
-    for (int t = 0; t < pre; ++t) fast_fetch(stage(t), L, t * kFBK);
-    __builtin_amdgcn_s_waitcnt(0);
-    step_barrier();
-    // Waves 4-7 start one phase late.
-    const bool late = wave >= kFWaves / 2;
-    if (late) step_barrier();
-
-    // Every memory phase fetches: past the last step it fetches the last step
-    // again, into the stage of step t-1, which no wave reads any more. After
-    // the fetch of step t+3 this wave has the fetches of steps t+1..t+3 in
-    // flight and waits for the oldest, which the other group reads two
-    // phases later.
-    const int last = (steps - 1) * kFBK;
-    for (int t = 0; t < steps; ++t) {
-        fast_memory_phase(stage(t), stage(t + 3), L, min((t + 3) * kFBK, last), av, bv);
-        __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kFFetchPerStep));  // vmcnt(8), lgkmcnt(0)
-        step_barrier();
-#pragma unroll
-        for (int fi = 0; fi < kFRowFrags; ++fi)
-#pragma unroll
-            for (int fj = 0; fj < kFColFrags; ++fj) acc[fi][fj] = mfma<kBf16>(bv[fj], av[fi], acc[fi][fj]);
-        step_barrier();
-    }
-    if (!late) step_barrier();
-    __builtin_amdgcn_s_waitcnt(0);
-
-    // acc[fi][fj] holds C[row0 + wr + 16 fi + l % 16][col0 + wc + 16 fj + 4 (l / 16) + v].
-#pragma unroll
-    for (int fi = 0; fi < kFRowFrags; ++fi) {
-        const int row = row0 + wr + fi * 16 + li;
-        if (row >= m) continue;
-        float* crow = c + static_cast<std::ptrdiff_t>(row) * n;
-#pragma unroll
-        for (int fj = 0; fj < kFColFrags; ++fj) {
-            const int col = col0 + wc + fj * 16 + 4 * g;
-            if (col < n) *reinterpret_cast<f32x4*>(crow + col) = acc[fi][fj];
-        }
-    }
+    mc_gemm16_fast<kBf16>(a, b, c, m, n, k, McGemm16Store{});
 }
 
 // The fast path takes 16-bit A and B with K a multiple of 64, N a multiple

@@ -7,5 +7,8 @@ namespace minicompiler::hip {
 
 // gemm_f32_mfma.h: the FP32 matrix-core GEMM body with an epilogue hook.
 extern const char* const kGemmF32MfmaSource;
+// gemm_mfma16_fast.h: the bf16 / fp16 matrix-core GEMM body (16-bit inputs
+// in HBM) with an epilogue hook.
+extern const char* const kGemm16FastSource;
 
 }  // namespace minicompiler::hip

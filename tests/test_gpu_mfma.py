@@ -69,3 +69,46 @@ def test_pre_cast_gemm_at_8192_cubed_on_sampled_elements(device, mc, oracle, ker
     assert np.all(np.abs(got - exact) <= lowp_gemm_bound(exact, absdot, k, u, subnormals))
     # BASELINE's own tolerance against the unrounded fp32 inputs: sqrt(K) 2^-8 max|a| max|b|.
     assert np.max(np.abs(got - exact)) <= np.sqrt(k) * (2.0 ** -8 if dtype == 1 else 2.0 ** -11)
+
+
+GRAPH_SHAPES = [(300, 256, 520), (256, 512, 256), (64, 64, 8)]
+
+
+@pytest.mark.parametrize("kernel", ["tensor_core_bf16", "tensor_core_f16"])
+@pytest.mark.parametrize("m,k,n", GRAPH_SHAPES)
+def test_graph_tensor_core_matmuls_convert_then_run_the_fast_kernel_bit_for_bit(device, mc, oracle, kernel, m, k, n):
+    # A compiled graph rounds fp32 operands to 16 bits into workspace (a
+    # constant weight once, the input per run) and runs the 256x256 kernel:
+    # the same bits as the kernel that rounds while staging, with K unsplit;
+    # with a bias+GELU group fused into its store, the same bits as the
+    # separate kernels.
+    print(f"case {kernel} {m}x{k}x{n}", flush=True)
+    text = (f"input x : f32[{m}, {k}]\nconst w : f32[{k}, {n}] = uniform(seed=2, lo=-1, hi=1)\n"
+            f"const bias : f32[{n}] = uniform(seed=3, lo=-0.01, hi=0.01)\nconst half : f32[] = 0.5\n"
+            "const one : f32[] = 1.0\nconst c : f32[] = 0.7978846\nconst coef : f32[] = 0.044715\n"
+            "h = matmul x, w\nhb = add h, bias\nx2 = mul hb, hb\nx3 = mul x2, hb\nt = mul x3, coef\n"
+            "u0 = add hb, t\nu = mul u0, c\nth = tanh u\np = add th, one\nhh = mul hb, half\ny = mul hh, p\noutput y\n")
+    x = oracle.uniform(m * k, 1, -1.0, 1.0)
+    runs = {}
+    for name, opts in (("fast+fused", {}), ("fast", {"epilogue": 0})):
+        c = mc.Compiled(text, options={"matmul": kernel, **opts})
+        assert c.matmul_kernels == [kernel]
+        runs[name] = (c, c.run([x])[0])
+    assert any(len(ids) > 1 for ids in runs["fast+fused"][0].launch_nodes)
+    assert np.array_equal(runs["fast+fused"][1].view(np.uint32), runs["fast"][1].view(np.uint32))
+    # The GEMM alone (weights an input, converted per run) against the
+    # operator-level staging kernel on the same fp32 operands, one split:
+    # the same rounding and the same accumulation order, so identical bits.
+    mm = f"input x : f32[{m}, {k}]\ninput w : f32[{k}, {n}]\nh = matmul x, w\noutput h\n"
+    w = oracle.uniform(k * n, 9, -1.0, 1.0)
+    g32 = mc.Compiled(mm, options={"matmul": kernel}).run([x, w])[0]
+    dx, dw = mc.DeviceBuffer.from_array(x), mc.DeviceBuffer.from_array(w)
+    dc = mc.DeviceBuffer.from_array(np.full(m * n, np.nan, np.float32))
+    mc.launch_matmul(kernel, dx.ptr, dw.ptr, dc.ptr, m, n, k)
+    mc.synchronize()
+    assert np.array_equal(g32.view(np.uint32), dc.download().view(np.uint32)), "staging kernel"
+    # And within the precision bound of the bf16/fp16 product against float64.
+    g = g32.astype(np.float64)
+    u, sub = (2.0 ** -8, False) if "bf16" in kernel else (2.0 ** -11, True)
+    exact, absdot = oracle.gemm_f64(x, w, m, k, n)
+    assert np.all(np.abs(g - exact) <= lowp_gemm_bound(exact, absdot, k, u, sub))

@@ -26,7 +26,7 @@ struct McGemm16Store {
     __device__ __forceinline__ float operator()(float v, unsigned) const { return v; }
 };
 
-// // 16-bit inputs already in HBM, K a multiple of 64, N a multiple of 8, rows
+// 16-bit inputs already in HBM, K a multiple of 64, N a multiple of 8, rows
 // 16-byte aligned. Block tile 256x256, 512 lanes = 8 waves in a 2x4 grid
 // (two waves per SIMD), each wave a 128x64 quadrant as 8x4 accumulators of
 // v_mfma_f32_16x16x32 (128 fp32 per lane, in AGPRs). One block per CU; the

@@ -156,7 +156,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
                                                  GemmBody body) {
     const std::size_t num_inputs = input_shapes.size();
     std::ostringstream os;
-    os << "// minicompiler-hip " << (body == GemmBody::F32Mfma ? "FP32" : body == GemmBody::Bf16Fast ? "bf16" : "fp16")
+    os << "// minicompiler-hip " << (is_f32_body(body) ? "FP32" : body == GemmBody::Bf16Fast ? "bf16" : "fp16")
        << " GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
        << to_string(out_shape) << ".\n";
     os << gemm_body_source << "\n";
@@ -191,7 +191,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         }
     }
     os << ");\n\t}\n};\n\n";
-    if (body != GemmBody::F32Mfma) {
+    if (!is_f32_body(body)) {
         os << "extern \"C\" __global__ void __launch_bounds__(512, 1)\n" << kGemmEpilogueKernelName
            << "(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b, float* __restrict__ c, "
               "int m, int n, int k, McEpilogue epi)\n{\n"
@@ -199,11 +199,17 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
            << ">(a, b, c, m, n, k, epi);\n}\n";
         return {os.str()};
     }
-    os << "extern \"C\" __global__ void __launch_bounds__(256, 2)\n" << kGemmEpilogueKernelName
+    const char* bounds = body == GemmBody::F32RingDeep ? "512, 1" : "256, 2";
+    os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
-          "int k_split, float* __restrict__ partial, McEpilogue epi)\n{\n"
-       << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false")
-       << ">(a, b, c, m, n, k, k_split, partial, epi);\n}\n\n";
+          "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n";
+    if (body == GemmBody::F32Mfma) {
+        os << "\t(void)depth;\n\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false")
+           << ">(a, b, c, m, n, k, k_split, partial, epi);\n}\n\n";
+    } else {
+        os << "\tmc_gemm_f32_ring<" << (body == GemmBody::F32RingDeep ? "McRingDeep" : "McRingWide")
+           << ">(a, b, c, m, n, k, k_split, depth, partial, epi);\n}\n\n";
+    }
     // Split K: the partial sums added in split order, then the epilogue.
     os << "extern \"C\" __global__ void __launch_bounds__(256)\n" << kSumSplitsEpilogueKernelName
        << "(const float* __restrict__ partial, float* __restrict__ c, unsigned count, int splits, McEpilogue epi)\n{\n"

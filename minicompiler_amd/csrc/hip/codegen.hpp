@@ -72,20 +72,27 @@ struct GemmEpilogueKernel {
 
 // Which GEMM body the epilogue kernel wraps.
 enum class GemmBody {
-    F32Mfma,   // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K
-    Bf16Fast,  // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
-    F16Fast,   // fp16 operands, likewise
+    F32Mfma,      // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K (gemm_f32_mfma.h)
+    F32RingWide,  // the same arithmetic, LDS ring, persistent: 256 lanes, 2 stages, two blocks per CU (gemm_f32_ring.h)
+    F32RingDeep,  // likewise, 512 lanes, 4 stages, one block per CU
+    Bf16Fast,     // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
+    F16Fast,      // fp16 operands, likewise
 };
+
+inline bool is_f32_body(GemmBody body) {
+    return body == GemmBody::F32Mfma || body == GemmBody::F32RingWide || body == GemmBody::F32RingDeep;
+}
 
 // A GEMM (the matrix-core body in `gemm_body_source`, of kind `body`) whose
 // store applies `program`, the
 // fused elementwise group that consumes the GEMM's result: the program's
 // input `acc_input` is the accumulated value; every other input is read at
 // the flat output index by its access class against `out_shape`. Kernel
-// arguments, FP32 body (grid (N/128, M/128, splits), 256 lanes):
-// (a, b, c, m, n, k, k_split, partial, epi) and, for split K, (partial, c,
-// count, splits, epi); 16-bit bodies (one block of 512 lanes per 256x256
-// tile): (a, b, c, m, n, k, epi). epi holds one float pointer per program
+// arguments, FP32 bodies: (a, b, c, m, n, k, k_split, depth, partial, epi)
+// (two-stage: grid (N/128, M/128, depth) of 256 lanes; ring: the grid and
+// block of mchip_f32_ring_plan) and, for split K, (partial, c, count, depth,
+// epi); 16-bit bodies (one block of 512 lanes per 256x256 tile): (a, b, c,
+// m, n, k, epi). epi holds one float pointer per program
 // input (that of `acc_input` unused). `vectorized_operands` (FP32): A and B
 // rows allow 16-byte loads (k and n multiples of 4, 16-byte aligned).
 GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,

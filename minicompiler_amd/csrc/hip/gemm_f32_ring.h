@@ -1,0 +1,320 @@
+// FP32 matrix-core GEMM body for gfx950 (v_mfma_f32_32x32x2_f32) with an LDS
+// ring fed by direct global -> LDS loads and persistent blocks that walk
+// their tiles in sequence. Shared by the ahead-of-time kernels
+// (matmul_fp32.hip, identity epilogue) and the GEMMs compiled at run time
+// with a fused elementwise epilogue. Self-contained: no standard or HIP
+// headers, so hipRTC compiles it as is.
+//
+// Same arithmetic as the two-stage body in gemm_f32_mfma.h: each C element
+// is accumulated by the same v_mfma_f32_32x32x2_f32 sequence (the 32-wide K
+// step split into k and k + 16 slot pairs, four k per LDS read), so every
+// configuration here and that body give identical bits, and any of them may
+// serve a request they all accept.
+//
+// Requirements (checked by the host): K (and the split size) a multiple of
+// 32, N a multiple of 4, A and B 16-byte aligned, every split non-empty. Rows past M and columns past N are clamped to the last row /
+// column chunk, so every load is in bounds; what they bring only reaches C
+// elements that are not stored.
+#pragma once
+
+typedef float mc_ring_f32x4 __attribute__((ext_vector_type(4)));
+typedef float mc_ring_f32x16 __attribute__((ext_vector_type(16)));
+#define MC_RING_LDS __attribute__((address_space(3)))
+
+// A configuration: block tile kBM x 128, K step 32, kWaves waves each owning
+// a kWM x kWN quadrant as (kWM / 32) x (kWN / 32) 32x32 accumulators, and a
+// ring of kStages LDS stages. Each wave's accumulators are independent MFMA
+// chains: a wave that runs alone at the end of a step keeps the matrix unit
+// busy only with enough of them (four measured enough, two not).
+template <int kBM_, int kWM_, int kWN_, int kWaves_, int kStages_>
+struct McRingCfg {
+    static constexpr int kBM = kBM_, kBN = 128, kBK = 32;
+    static constexpr int kWM = kWM_, kWN = kWN_, kWaves = kWaves_, kStages = kStages_;
+    static constexpr int kThreads = kWaves * 64;
+    static constexpr int kWavesN = kBN / kWN;
+    static constexpr int kAI = kWM / 32, kBJ = kWN / 32;
+    static constexpr int kABytes = kBM * kBK * 4;
+    static constexpr int kStage = kABytes + kBK * kBN * 4;
+    // 1 KiB fetch blocks per wave and step: A has kBM / 8, B 16.
+    static constexpr int kFA = kBM / 8 / kWaves, kFB = 16 / kWaves;
+    static constexpr int kFetch = kFA + kFB;
+    static constexpr int kLds = kStages * kStage;
+    static_assert((kBM / kWM) * kWavesN == kWaves, "waves tile the block");
+    static_assert(kFA * kWaves * 8 == kBM && kFB * kWaves == 16, "fetch blocks split evenly");
+};
+
+// The two configurations the library runs (mchip_f32_ring_plan picks one):
+// two blocks of 4 waves (64x64 quadrants) with 2 stages per CU, for products
+// with at least two tiles per CU, and one block of 8 waves (64x32) with 4
+// stages per CU otherwise.
+using McRingWide = McRingCfg<128, 64, 64, 4, 2>;
+using McRingDeep = McRingCfg<128, 64, 32, 8, 4>;
+
+// LDS layout of a stage (bytes):
+//   A at 0: kBM / 8 blocks of 1 KiB, block rb holding rows 8 rb .. 8 rb + 7
+//     of the tile. Chunk c (k 4c .. 4c + 3, 16 bytes) of row r sits at
+//     position p = 16 (c / 2) + 8 ((c % 2) ^ (rb % 2)) + r % 8 of its block.
+//     An A-fragment read (32 lanes: 32 consecutive rows, one chunk) then
+//     puts every 16 lanes on 16 distinct 16-byte bank groups; a fetch
+//     instruction (lane l -> position l) still covers 8 whole 128-byte rows.
+//   B after A: k row kk at 512 kk, n-contiguous, its 16-byte chunk g stored
+//     at g ^ 8 (kk / 16 % 2), so the two half-waves of a read (k rows kk and
+//     kk + 16, the same 32 columns) use disjoint banks.
+
+__device__ __forceinline__ int mc_ring_min(int a, int b) { return a < b ? a : b; }
+
+// Where this lane's fetches of one step come from, for one unit (a tile, or
+// a tile's share of K under split-K).
+template <class Cfg>
+struct McRingFetch {
+    const float* a_src[Cfg::kFA];
+    const float* b_src[Cfg::kFB];
+    long long b_step;  // elements between consecutive K steps of B
+};
+
+struct McRingUnit {
+    int row0, col0, kb, steps, split;
+};
+
+// Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
+// 16 bytes at (LDS base + 16 l).
+template <class Cfg>
+__device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
+                                              int t) {
+    MC_RING_LDS unsigned char* sa = wr + wave * Cfg::kFA * 1024;
+    MC_RING_LDS unsigned char* sb = wr + Cfg::kABytes + wave * Cfg::kFB * 1024;
+#pragma unroll
+    for (int i = 0; i < Cfg::kFA; ++i) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.a_src[i] + t * Cfg::kBK),
+                                         reinterpret_cast<MC_RING_LDS void*>(sa + i * 1024), 16, 0, 0);
+    }
+    const long long bo = t * f.b_step;
+#pragma unroll
+    for (int i = 0; i < Cfg::kFB; ++i) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.b_src[i] + bo),
+                                         reinterpret_cast<MC_RING_LDS void*>(sb + i * 1024), 16, 0, 0);
+    }
+}
+
+// One step: optionally fetch a later step into `wr`, then multiply the step
+// held in `rd` (the MFMA sequence of the two-stage body). `rd` and `wr` are
+// distinct stages; declaring them __restrict__ gives the LDS reads alias
+// scopes that keep the compiler from making them wait for the fetch.
+template <class Cfg>
+__device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __restrict__ rd,
+                                             MC_RING_LDS unsigned char* __restrict__ wr, bool do_fetch,
+                                             const McRingFetch<Cfg>& f, int wave, int fetch_t,
+                                             const int (&a_off)[Cfg::kAI][4], const int (&b_off)[Cfg::kBJ],
+                                             mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ]) {
+    if (do_fetch) mc_ring_fetch<Cfg>(wr, f, wave, fetch_t);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        mc_ring_f32x4 av[Cfg::kAI];
+#pragma unroll
+        for (int i = 0; i < Cfg::kAI; ++i) av[i] = *reinterpret_cast<const MC_RING_LDS mc_ring_f32x4*>(rd + a_off[i][q]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float bv[Cfg::kBJ];
+#pragma unroll
+            for (int j = 0; j < Cfg::kBJ; ++j)
+                bv[j] = *reinterpret_cast<const MC_RING_LDS float*>(rd + b_off[j] + (q * 4 + e) * 512);
+#pragma unroll
+            for (int i = 0; i < Cfg::kAI; ++i)
+#pragma unroll
+                for (int j = 0; j < Cfg::kBJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j], acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
+// s_waitcnt vmcnt(v) lgkmcnt(0), expcnt not waited on (gfx9 encoding).
+#define MC_RING_WAIT(v) __builtin_amdgcn_s_waitcnt(0x0070 | ((v) & 15) | (((v) >> 4) << 14))
+
+// A workgroup barrier without a memory fence; the compiler may not move
+// memory operations or MFMAs across it.
+__device__ __forceinline__ void mc_ring_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The C tiles (and K splits) of an M x N x K product, `splits` splits of
+// `k_split` each: unit u is split u / tiles of tile u % tiles (tiles in
+// row-major order). Blocks are persistent: with the grid a multiple of 8,
+// block b runs on XCD b % 8 and takes the units of that XCD's contiguous
+// eighth of the list, so the blocks sharing an XCD's L2 share A row bands
+// and B column panels; otherwise block b takes units b, b + grid, ...
+// With one split the epilogue maps each accumulated value v of element
+// i = row n + col to what is stored; with several, the raw partial sums go
+// to `partial` (split s at s m n) and the epilogue is applied where the
+// splits are summed.
+template <class Cfg, typename Epilogue>
+__device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, const float* __restrict__ b,
+                                                 float* __restrict__ c, int m, int n, int k, int k_split, int splits,
+                                                 float* __restrict__ partial, const Epilogue& epilogue) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[Cfg::kLds];
+    MC_RING_LDS unsigned char* lds = (MC_RING_LDS unsigned char*)(smem);  // generic -> LDS address space
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int tiles_n = (n + Cfg::kBN - 1) / Cfg::kBN;
+    const int tiles = ((m + Cfg::kBM - 1) / Cfg::kBM) * tiles_n;
+    const int units = tiles * splits;
+
+    // This block's units: first, first + stride, ... (count of them).
+    const int grid = static_cast<int>(gridDim.x);
+    int first, stride, count;
+    if (grid % 8 == 0) {
+        const int x = static_cast<int>(blockIdx.x) % 8, j = static_cast<int>(blockIdx.x) / 8;
+        const int lo = static_cast<int>(static_cast<long long>(x) * units / 8);
+        const int hi = static_cast<int>(static_cast<long long>(x + 1) * units / 8);
+        first = lo + j;
+        stride = grid / 8;
+        count = first < hi ? (hi - first + stride - 1) / stride : 0;
+    } else {
+        first = static_cast<int>(blockIdx.x);
+        stride = grid;
+        count = first < units ? (units - first + stride - 1) / stride : 0;
+    }
+    auto unit_of = [&](int i) {
+        const int u = first + i * stride;
+        McRingUnit r;
+        r.split = u / tiles;
+        const int t = u % tiles;
+        r.row0 = (t / tiles_n) * Cfg::kBM;
+        r.col0 = (t % tiles_n) * Cfg::kBN;
+        r.kb = r.split * k_split;
+        const int ke = mc_ring_min(k, r.kb + k_split);
+        r.steps = (ke - r.kb) / Cfg::kBK;
+        return r;
+    };
+    // A: wave w fills blocks rb = kFA w + i; lane l -> row 8 rb + l % 8,
+    // chunk 2 (l / 16) + ((l / 8 % 2) ^ (rb % 2)). B: wave w fills blocks
+    // bb = kFB w + i, k rows 2 bb and 2 bb + 1; lane l -> k row 2 bb + l / 32,
+    // logical chunk (l % 32) ^ 8 (k row / 16 % 2).
+    auto fetch_of = [&](const McRingUnit& u) {
+        McRingFetch<Cfg> f;
+#pragma unroll
+        for (int i = 0; i < Cfg::kFA; ++i) {
+            const int rb = Cfg::kFA * wave + i;
+            const int r = mc_ring_min(u.row0 + rb * 8 + (lane & 7), m - 1);
+            const int ch = 2 * (lane >> 4) + (((lane >> 3) & 1) ^ (rb & 1));
+            f.a_src[i] = a + static_cast<long long>(r) * k + u.kb + 4 * ch;
+        }
+#pragma unroll
+        for (int i = 0; i < Cfg::kFB; ++i) {
+            const int kk = 2 * (Cfg::kFB * wave + i) + (lane >> 5);
+            const int g = (lane & 31) ^ (8 * ((kk >> 4) & 1));
+            const int col = mc_ring_min(u.col0 + 4 * g, n - 4);
+            f.b_src[i] = b + static_cast<long long>(u.kb + kk) * n + col;
+        }
+        f.b_step = static_cast<long long>(Cfg::kBK) * n;
+        return f;
+    };
+
+    // Read offsets. Wave (wm, wn) owns rows kWM wm .. and columns kWN wn ..;
+    // lane l reads A rows wr + 32 i + l % 32 and B columns wc + 32 j + l % 32,
+    // k slot l / 32.
+    const int wr = (wave / Cfg::kWavesN) * Cfg::kWM, wc = (wave % Cfg::kWavesN) * Cfg::kWN;
+    const int half = lane >> 5, li = lane & 31;
+    int a_off[Cfg::kAI][4];
+#pragma unroll
+    for (int i = 0; i < Cfg::kAI; ++i) {
+        const int row = wr + 32 * i + li;
+        const int rb = row >> 3;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int ch = 4 * half + q;
+            a_off[i][q] = rb * 1024 + 16 * (16 * (ch >> 1) + 8 * ((ch & 1) ^ (rb & 1)) + (row & 7));
+        }
+    }
+    int b_off[Cfg::kBJ];
+#pragma unroll
+    for (int j = 0; j < Cfg::kBJ; ++j) {
+        const int bcol = wc + 32 * j + li;
+        b_off[j] = Cfg::kABytes + half * 16 * 512 + (((bcol >> 2) ^ (8 * half)) << 4) + (bcol & 3) * 4;
+    }
+
+    // Total steps of this block, and the fetch cursor (unit fi, step ft).
+    int total = 0;
+    for (int i = 0; i < count; ++i) total += unit_of(i).steps;
+    int fi = 0, ft = 0;
+    McRingUnit fu = unit_of(0);
+    McRingFetch<Cfg> fetch = fetch_of(fu);
+    auto advance = [&]() {
+        if (++ft == fu.steps) {
+            ft = 0;
+            if (++fi < count) {
+                fu = unit_of(fi);
+                fetch = fetch_of(fu);
+            }
+        }
+    };
+
+    // Stage of the next fetch and of the next step to multiply.
+    int ws = 0, rs = 0;
+    auto next = [](int s) { return s + 1 == Cfg::kStages ? 0 : s + 1; };
+    int issued = 0;
+    const int pre = mc_ring_min(total, Cfg::kStages - 1);
+    for (; issued < pre; ++issued) {
+        mc_ring_fetch<Cfg>(lds + ws * Cfg::kStage, fetch, wave, ft);
+        ws = next(ws);
+        advance();
+    }
+
+    int g = 0;  // steps consumed
+    for (int ui = 0; ui < count; ++ui) {
+        const McRingUnit u = unit_of(ui);
+        mc_ring_f32x16 acc[Cfg::kAI][Cfg::kBJ];
+#pragma unroll
+        for (int i = 0; i < Cfg::kAI; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::kBJ; ++j) acc[i][j] = mc_ring_f32x16{};
+        for (int t = 0; t < u.steps; ++t, ++g) {
+            // Fetch groups issued after the one of step g (stores issued
+            // after it only make the wait longer): wait for that one and for
+            // this wave's LDS reads of the previous step.
+            const int later = issued - g - 1;
+            if (later >= 2) {
+                MC_RING_WAIT(2 * Cfg::kFetch);
+            } else if (later == 1) {
+                MC_RING_WAIT(Cfg::kFetch);
+            } else {
+                MC_RING_WAIT(0);
+            }
+            // Every wave's fetch of step g has landed, and every wave is done
+            // with step g - 1, whose stage the next fetch overwrites.
+            mc_ring_barrier();
+            const bool more = issued < total;
+            mc_ring_step<Cfg>(lds + rs * Cfg::kStage, lds + ws * Cfg::kStage, more, fetch, wave, ft, a_off, b_off, acc);
+            rs = next(rs);
+            if (more) {
+                ++issued;
+                ws = next(ws);
+                advance();
+            }
+        }
+
+        // acc[i][j] value v of lane l: row wr + 32 i + 8 (v / 4) + 4 (l / 32) + v % 4,
+        // column wc + 32 j + l % 32.
+        float* __restrict__ out = splits > 1 ? partial + static_cast<long long>(u.split) * m * n : c;
+#pragma unroll
+        for (int j = 0; j < Cfg::kBJ; ++j) {
+            const int col = u.col0 + wc + 32 * j + li;
+            if (col >= n) continue;
+#pragma unroll
+            for (int i = 0; i < Cfg::kAI; ++i) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = u.row0 + wr + 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (row >= m) continue;
+                    const long long at = static_cast<long long>(row) * n + col;
+                    out[at] = splits > 1 ? acc[i][j][v] : epilogue(acc[i][j][v], static_cast<unsigned>(at));
+                }
+            }
+        }
+    }
+    MC_RING_WAIT(0);
+}

@@ -70,8 +70,9 @@ struct Launch {
     int m = 0, n = 0, k = 0;
     // FusedMatmul: generated kernels and their stable arguments.
     void* sum_function = nullptr;
-    unsigned grid_x = 0, grid_y = 0, grid_z = 0, sum_grid = 0;
-    int k_split = 0;
+    unsigned grid_x = 0, grid_y = 0, grid_z = 0, sum_grid = 0, block = 256;
+    int k_split = 0, depth = 1;
+    GemmBody body = GemmBody::F32Mfma;
     const void* a_ptr = nullptr;
     const void* b_ptr = nullptr;
     void* c_ptr = nullptr;
@@ -155,6 +156,7 @@ public:
                     l.kind = Launch::Kind::FusedMatmul;
                     l.epilogue_node = f;
                     fused_away[static_cast<std::size_t>(f)] = true;
+                    l.body = fused_body(l);
                 }
                 const std::size_t ws =
                     l.lowp ? align_up(static_cast<std::size_t>(l.m) * l.k * 2) + align_up(static_cast<std::size_t>(l.k) * l.n * 2)
@@ -410,9 +412,9 @@ private:
             return Status();
         }
         if (l.kind == Launch::Kind::FusedMatmul) {
-            int rc = mchip_module_launch3(l.function, l.grid_x, l.grid_y, l.grid_z, 256, 0, s, l.params.data());
+            int rc = mchip_module_launch3(l.function, l.grid_x, l.grid_y, l.grid_z, l.block, 0, s, l.params.data());
             if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
-            if (l.grid_z > 1) {
+            if (l.depth > 1) {
                 rc = mchip_module_launch(l.sum_function, l.sum_grid, 256, 0, s, l.sum_params.data());
                 if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_sum_splits_epilogue)");
             }
@@ -459,6 +461,21 @@ private:
             l->convert_b = graph_.node(node.inputs[1]).op != OpKind::Constant;
         }
         return Status();
+    }
+
+    // The GEMM body of a fused matmul, chosen as mchip_launch_matmul chooses
+    // for the same kernel (operands in the arena or bound by the caller are
+    // 16-byte aligned).
+    GemmBody fused_body(Launch& l) const {
+        if (l.lowp) return l.dtype == MCHIP_DTYPE_BF16 ? GemmBody::Bf16Fast : GemmBody::F16Fast;
+        split_layout(l.k, l.splits, &l.k_split, &l.depth);
+        if (l.matmul == MatmulKernel::Vectorized || l.k % 4 != 0) return GemmBody::F32Mfma;
+        unsigned grid = 0, block = 0;
+        switch (mchip_f32_ring_plan(l.m, l.n, l.k, l.depth, device_.cu_count, &grid, &block)) {
+            case MCHIP_RING_WIDE: return GemmBody::F32RingWide;
+            case MCHIP_RING_DEEP: return GemmBody::F32RingDeep;
+            default: return GemmBody::F32Mfma;
+        }
     }
 
     // The fused elementwise group this matmul's store can apply, or kNoNode.
@@ -528,10 +545,12 @@ private:
                     if (f.inputs[k] == l.node) acc = k;
                 }
                 ElementwiseKernel k;
-                const GemmBody body = !l.lowp ? GemmBody::F32Mfma
-                                      : l.dtype == MCHIP_DTYPE_BF16 ? GemmBody::Bf16Fast : GemmBody::F16Fast;
+                const GemmBody body = l.body;
+                const char* body_source = l.lowp                        ? kGemm16FastSource
+                                          : body == GemmBody::F32Mfma ? kGemmF32MfmaSource
+                                                                      : kGemmF32RingSource;
                 k.source = generate_gemm_epilogue_kernel(*f.fused, acc, shapes, f.type.shape, l.n % 4 == 0 && l.k % 4 == 0,
-                                                         l.lowp ? kGemm16FastSource : kGemmF32MfmaSource, body)
+                                                         body_source, body)
                                .source;
                 jobs.push_back({j, std::move(k)});
                 continue;
@@ -583,15 +602,22 @@ private:
                                                                             arch, dev, nullptr);
                 if (!sum.ok()) return sum.error();
                 l.sum_function = sum->function;
-                int depth = 1;
-                split_layout(l.k, l.splits, &l.k_split, &depth);
-                l.grid_x = static_cast<unsigned>((l.n + 127) / 128);
-                l.grid_y = static_cast<unsigned>((l.m + 127) / 128);
-                l.grid_z = static_cast<unsigned>(depth);
+                if (l.body == GemmBody::F32Mfma) {
+                    l.grid_x = static_cast<unsigned>((l.n + 127) / 128);
+                    l.grid_y = static_cast<unsigned>((l.m + 127) / 128);
+                    l.grid_z = static_cast<unsigned>(l.depth);
+                    l.block = 256;
+                } else {
+                    unsigned grid = 0, block = 0;
+                    mchip_f32_ring_plan(l.m, l.n, l.k, l.depth, device_.cu_count, &grid, &block);
+                    l.grid_x = grid;
+                    l.grid_y = l.grid_z = 1;
+                    l.block = block;
+                }
                 l.count = static_cast<unsigned>(static_cast<std::size_t>(l.m) * l.n);
                 l.sum_grid = static_cast<unsigned>(std::max<std::size_t>(
                     1, std::min<std::size_t>((static_cast<std::size_t>(l.count) + 255) / 256, 8192)));
-                l.partial = depth > 1 ? l.workspace : nullptr;
+                l.partial = l.depth > 1 ? l.workspace : nullptr;
                 l.epilogue_inputs.assign(graph_.node(l.epilogue_node).inputs.size(), nullptr);
                 continue;
             }
@@ -616,9 +642,9 @@ private:
                 continue;
             }
             if (l.kind == Launch::Kind::FusedMatmul) {
-                l.params = {&l.a_ptr, &l.b_ptr, &l.c_ptr, &l.m, &l.n, &l.k, &l.k_split, &l.partial,
+                l.params = {&l.a_ptr, &l.b_ptr, &l.c_ptr, &l.m, &l.n, &l.k, &l.k_split, &l.depth, &l.partial,
                             l.epilogue_inputs.data()};
-                l.sum_params = {&l.partial, &l.c_ptr, &l.count, &l.grid_z, l.epilogue_inputs.data()};
+                l.sum_params = {&l.partial, &l.c_ptr, &l.count, &l.depth, l.epilogue_inputs.data()};
                 continue;
             }
             if (l.kind != Launch::Kind::Elementwise) continue;

@@ -12,14 +12,22 @@
 //                      loads are in flight during the current tile's MFMAs
 //   split_k            double_buffered with K split over the grid's depth and
 //                      a fixed-order (deterministic) sum of the partials
+//
+// double_buffered and split_k run the ring body (gemm_f32_ring.h) where the
+// shape allows: direct global -> LDS loads, persistent blocks walking their
+// tiles (and K splits) with an XCD-aware order, two stages and two blocks per
+// CU when there are enough tiles, else four stages and one 8-wave block per
+// CU. Its arithmetic is the two-stage body's, bit for bit.
 
 #include "matmul.h"
 
 #include <hip/hip_runtime.h>
 
 #include "gemm_f32_mfma.h"
+#include "gemm_f32_ring.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
@@ -146,6 +154,17 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
     mc_gemm_f32_mfma<kDouble, kVec>(a, b, c, m, n, k, k_split, partial, McGemmStore{});
 }
 
+using RingWide = McRingWide;
+using RingDeep = McRingDeep;
+constexpr int kRBKRing = RingWide::kBK;
+
+template <class Cfg, int kBlocksPerCu>
+__global__ void __launch_bounds__(Cfg::kThreads, kBlocksPerCu)
+    matmul_ring_f32(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n,
+                    int k, int k_split, int depth, float* __restrict__ partial) {
+    mc_gemm_f32_ring<Cfg>(a, b, c, m, n, k, k_split, depth, partial, McGemmStore{});
+}
+
 // ---------------------------------------------------------------- split-K sum
 
 __global__ void __launch_bounds__(256) sum_splits(const float* __restrict__ partial, float* __restrict__ c,
@@ -176,6 +195,21 @@ int split_len(int k, int splits, int step) {
     return (per + step - 1) / step * step;
 }
 
+// CUs of the current device, asked once per device.
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
 int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
                     hipStream_t stream, int splits, float* workspace) {
     const int k_split = split_len(k, splits, kMBK);
@@ -184,7 +218,16 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     const dim3 grid((n + kMBN - 1) / kMBN, (m + kMBM - 1) / kMBM, depth);
     const bool vec = n % 4 == 0 && k % 4 == 0 && aligned16(a) && aligned16(b);
     float* out_ws = depth > 1 ? workspace : nullptr;
-    if (double_buffer) {
+    unsigned ring_grid = 0, ring_block = 0;
+    const int ring = double_buffer && vec ? mchip_f32_ring_plan(m, n, k, depth, device_cu_count(), &ring_grid, &ring_block)
+                                          : MCHIP_RING_NONE;
+    if (ring == MCHIP_RING_WIDE) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws);
+    } else if (ring == MCHIP_RING_DEEP) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingDeep, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws);
+    } else if (double_buffer) {
         if (vec) {
             hipLaunchKernelGGL((matmul_mfma_f32<true, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
         } else {
@@ -203,6 +246,23 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
 }
 
 }  // namespace
+
+extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block) {
+    *grid = 0;
+    *block = 0;
+    if (m < 1 || n < 4 || k < kRBKRing || k % kRBKRing != 0 || n % 4 != 0 || depth < 1 || cu_count < 1) {
+        return MCHIP_RING_NONE;
+    }
+    const long long units = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
+    if (units >= 2LL * cu_count) {
+        *grid = static_cast<unsigned>(2 * cu_count);
+        *block = RingWide::kThreads;
+        return MCHIP_RING_WIDE;
+    }
+    *grid = static_cast<unsigned>(std::min<long long>(units, cu_count));
+    *block = RingDeep::kThreads;
+    return MCHIP_RING_DEEP;
+}
 
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);

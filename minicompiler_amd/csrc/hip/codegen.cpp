@@ -153,7 +153,7 @@ Access classify_access(const Shape& in, const Shape& out) {
 GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
                                                  const std::vector<Shape>& input_shapes, const Shape& out_shape,
                                                  bool vectorized_operands, const char* gemm_body_source,
-                                                 GemmBody body) {
+                                                 GemmBody body, const GemmDims& fixed) {
     const std::size_t num_inputs = input_shapes.size();
     std::ostringstream os;
     os << "// minicompiler-hip " << (is_f32_body(body) ? "FP32" : body == GemmBody::Bf16Fast ? "bf16" : "fp16")
@@ -191,24 +191,33 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         }
     }
     os << ");\n\t}\n};\n\n";
+    // The body's shape arguments: the kernel's own, or constants.
+    const bool constant = fixed.m > 0;
+    const std::string mnk = constant ? std::to_string(fixed.m) + ", " + std::to_string(fixed.n) + ", " +
+                                           std::to_string(fixed.k)
+                                     : std::string("m, n, k");
+    const std::string split = constant ? std::to_string(fixed.k_split) + ", " + std::to_string(fixed.depth)
+                                       : std::string("k_split, depth");
+    const char* unused = constant ? "\t(void)m;\n\t(void)n;\n\t(void)k;\n" : "";
     if (!is_f32_body(body)) {
         os << "extern \"C\" __global__ void __launch_bounds__(512, 1)\n" << kGemmEpilogueKernelName
            << "(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b, float* __restrict__ c, "
               "int m, int n, int k, McEpilogue epi)\n{\n"
-           << "\tmc_gemm16_fast<" << (body == GemmBody::Bf16Fast ? "true" : "false")
-           << ">(a, b, c, m, n, k, epi);\n}\n";
+           << unused << "\tmc_gemm16_fast<" << (body == GemmBody::Bf16Fast ? "true" : "false")
+           << ">(a, b, c, " << mnk << ", epi);\n}\n";
         return {os.str()};
     }
     const char* bounds = body == GemmBody::F32RingDeep ? "512, 1" : "256, 2";
     os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
-          "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n";
+          "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n"
+       << unused << (constant ? "\t(void)k_split;\n" : "") << "\t(void)depth;\n";
     if (body == GemmBody::F32Mfma) {
-        os << "\t(void)depth;\n\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false")
-           << ">(a, b, c, m, n, k, k_split, partial, epi);\n}\n\n";
+        os << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false") << ">(a, b, c, " << mnk
+           << ", " << (constant ? std::to_string(fixed.k_split) : std::string("k_split")) << ", partial, epi);\n}\n\n";
     } else {
-        os << "\tmc_gemm_f32_ring<" << (body == GemmBody::F32RingDeep ? "McRingDeep" : "McRingWide")
-           << ">(a, b, c, m, n, k, k_split, depth, partial, epi);\n}\n\n";
+        os << "\tmc_gemm_f32_ring<" << (body == GemmBody::F32RingDeep ? "McRingDeep" : "McRingWide") << ">(a, b, c, "
+           << mnk << ", " << split << ", partial, epi);\n}\n\n";
     }
     // Split K: the partial sums added in split order, then the epilogue.
     os << "extern \"C\" __global__ void __launch_bounds__(256)\n" << kSumSplitsEpilogueKernelName

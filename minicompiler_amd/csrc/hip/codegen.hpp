@@ -95,10 +95,18 @@ inline bool is_f32_body(GemmBody body) {
 // m, n, k, epi). epi holds one float pointer per program
 // input (that of `acc_input` unused). `vectorized_operands` (FP32): A and B
 // rows allow 16-byte loads (k and n multiples of 4, 16-byte aligned).
+// The product's dimensions, when the kernel serves one shape only: the
+// generated kernel then passes them to the body as constants (the index and
+// address arithmetic folds, e.g. a bias read once per column instead of per
+// element) and ignores its m, n, k, k_split and depth arguments.
+struct GemmDims {
+    int m = 0, n = 0, k = 0, k_split = 0, depth = 1;
+};
+
 GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, std::size_t acc_input,
                                                  const std::vector<Shape>& input_shapes, const Shape& out_shape,
                                                  bool vectorized_operands, const char* gemm_body_source,
-                                                 GemmBody body = GemmBody::F32Mfma);
+                                                 GemmBody body = GemmBody::F32Mfma, const GemmDims& fixed = {});
 
 // The generator options a compiled graph uses.
 CodegenOptions codegen_options(const HipOptions& options);

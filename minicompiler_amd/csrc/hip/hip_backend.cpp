@@ -151,7 +151,14 @@ public:
             if (node.op == OpKind::MatMul) {
                 Status st = plan_matmul(node, &l);
                 if (!st.ok()) return st;
-                const NodeId f = epilogue_for(id, l);
+                bool relocate = false;
+                const NodeId f = epilogue_for(id, l, &relocate);
+                if (f != kNoNode && relocate) {
+                    // The group's planned buffer is one the fused kernel reads:
+                    // its output gets arena space of its own instead.
+                    offset_[static_cast<std::size_t>(f)] = top;
+                    top += align_up(std::max<std::size_t>(graph_.node(f).type.size_bytes(), 4));
+                }
                 if (f != kNoNode) {
                     l.kind = Launch::Kind::FusedMatmul;
                     l.epilogue_node = f;
@@ -481,11 +488,13 @@ private:
     // The fused elementwise group this matmul's store can apply, or kNoNode.
     // Only when it is safe to run the group at the matmul's place: the group
     // is the next compute node, reads the product element for element (same
-    // element count) and is its only reader, the product is not a graph
-    // output, and the group's output buffer is none of the buffers the fused
-    // kernel reads (the memory plan may hand a buffer freed by the matmul's
-    // operands to the group's output).
-    NodeId epilogue_for(NodeId m, const Launch& l) const {
+    // element count) and is its only reader, and the product is not a graph
+    // output. The memory plan may hand a buffer freed by the matmul's
+    // operands (or by another input of the group) to the group's output; then
+    // *relocate is set and the output must be placed outside the plan's
+    // buffers, since the fused kernel still reads that buffer.
+    NodeId epilogue_for(NodeId m, const Launch& l, bool* relocate) const {
+        *relocate = false;
         if (!options_.fuse_epilogue) return kNoNode;
         if (!l.lowp && l.matmul != MatmulKernel::Vectorized && l.matmul != MatmulKernel::DoubleBuffered &&
             l.matmul != MatmulKernel::SplitK) {
@@ -517,12 +526,8 @@ private:
             if (node.op == OpKind::Input || node.op == OpKind::Constant) return false;
             return plan_.buffer_of[static_cast<std::size_t>(id)] == out_buffer;
         };
-        for (NodeId in : graph_.node(m).inputs) {
-            if (shares_output_buffer(in)) return kNoNode;
-        }
-        for (NodeId in : fn.inputs) {
-            if (in != m && shares_output_buffer(in)) return kNoNode;
-        }
+        for (NodeId in : graph_.node(m).inputs) *relocate = *relocate || shares_output_buffer(in);
+        for (NodeId in : fn.inputs) *relocate = *relocate || (in != m && shares_output_buffer(in));
         return f;
     }
 
@@ -549,8 +554,14 @@ private:
                 const char* body_source = l.lowp                        ? kGemm16FastSource
                                           : body == GemmBody::F32Mfma ? kGemmF32MfmaSource
                                                                       : kGemmF32RingSource;
+                GemmDims dims;
+                dims.m = l.m;
+                dims.n = l.n;
+                dims.k = l.k;
+                dims.k_split = l.k_split;
+                dims.depth = l.depth;
                 k.source = generate_gemm_epilogue_kernel(*f.fused, acc, shapes, f.type.shape, l.n % 4 == 0 && l.k % 4 == 0,
-                                                         body_source, body)
+                                                         body_source, body, dims)
                                .source;
                 jobs.push_back({j, std::move(k)});
                 continue;

@@ -73,14 +73,16 @@ struct GemmEpilogueKernel {
 // Which GEMM body the epilogue kernel wraps.
 enum class GemmBody {
     F32Mfma,      // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K (gemm_f32_mfma.h)
-    F32RingWide,  // the same arithmetic, LDS ring, persistent: 256 lanes, 2 stages, two blocks per CU (gemm_f32_ring.h)
-    F32RingDeep,  // likewise, 512 lanes, 4 stages, one block per CU
+    F32RingBig,   // the same arithmetic, LDS ring, persistent (gemm_f32_ring.h): 256x256 tiles, one block per CU
+    F32RingWide,  // likewise, 128x128 tiles, 2 stages, two blocks per CU
+    F32RingDeep,  // likewise, 128x128 tiles, 4 stages, one block per CU
     Bf16Fast,     // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
     F16Fast,      // fp16 operands, likewise
 };
 
 inline bool is_f32_body(GemmBody body) {
-    return body == GemmBody::F32Mfma || body == GemmBody::F32RingWide || body == GemmBody::F32RingDeep;
+    return body == GemmBody::F32Mfma || body == GemmBody::F32RingBig || body == GemmBody::F32RingWide ||
+           body == GemmBody::F32RingDeep;
 }
 
 // A GEMM (the matrix-core body in `gemm_body_source`, of kind `body`) whose

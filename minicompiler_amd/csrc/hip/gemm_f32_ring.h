@@ -12,43 +12,78 @@
 // serve a request they all accept.
 //
 // Requirements (checked by the host): K (and the split size) a multiple of
-// 32, N a multiple of 4, A and B 16-byte aligned, every split non-empty. Rows past M and columns past N are clamped to the last row /
-// column chunk, so every load is in bounds; what they bring only reaches C
-// elements that are not stored.
+// 32, N a multiple of 4, A, B and C 16-byte aligned, every split non-empty.
+// Rows past M and columns past N are clamped to the last row / column
+// chunk, so every load is in bounds; what they bring only reaches C elements
+// that are not stored.
 #pragma once
 
 typedef float mc_ring_f32x4 __attribute__((ext_vector_type(4)));
+typedef float mc_ring_f32x2 __attribute__((ext_vector_type(2)));
 typedef float mc_ring_f32x16 __attribute__((ext_vector_type(16)));
 #define MC_RING_LDS __attribute__((address_space(3)))
 
-// A configuration: block tile kBM x 128, K step 32, kWaves waves each owning
+// Float vectors of 1, 2 or 4 lanes, for B reads and C stores.
+template <int N>
+struct McRingVec;
+template <>
+struct McRingVec<1> {
+    typedef float type;
+    static __device__ __forceinline__ float get(type v, int) { return v; }
+    static __device__ __forceinline__ void set(type& v, int, float x) { v = x; }
+};
+template <>
+struct McRingVec<2> {
+    typedef mc_ring_f32x2 type;
+    static __device__ __forceinline__ float get(type v, int i) { return v[i]; }
+    static __device__ __forceinline__ void set(type& v, int i, float x) { v[i] = x; }
+};
+template <>
+struct McRingVec<4> {
+    typedef mc_ring_f32x4 type;
+    static __device__ __forceinline__ float get(type v, int i) { return v[i]; }
+    static __device__ __forceinline__ void set(type& v, int i, float x) { v[i] = x; }
+};
+
+// A configuration: block tile kBM x kBN, K step 32, kWaves waves each owning
 // a kWM x kWN quadrant as (kWM / 32) x (kWN / 32) 32x32 accumulators, and a
-// ring of kStages LDS stages. Each wave's accumulators are independent MFMA
-// chains: a wave that runs alone at the end of a step keeps the matrix unit
-// busy only with enough of them (four measured enough, two not).
-template <int kBM_, int kWM_, int kWN_, int kWaves_, int kStages_>
+// ring of kStages LDS stages. Lane l of a wave holds, for its accumulators'
+// column blocks j < kBJ, the columns wc + kBJ (l % 32) + j: one 4-, 8- or
+// 16-byte LDS read gives a lane the B values of all its column blocks, and C
+// is stored kBJ floats at a time. The MFMA sequence of each C element does
+// not depend on this assignment.
+template <int kBM_, int kBN_, int kWM_, int kWN_, int kWaves_, int kStages_>
 struct McRingCfg {
-    static constexpr int kBM = kBM_, kBN = 128, kBK = 32;
+    static constexpr int kBM = kBM_, kBN = kBN_, kBK = 32;
     static constexpr int kWM = kWM_, kWN = kWN_, kWaves = kWaves_, kStages = kStages_;
     static constexpr int kThreads = kWaves * 64;
     static constexpr int kWavesN = kBN / kWN;
     static constexpr int kAI = kWM / 32, kBJ = kWN / 32;
     static constexpr int kABytes = kBM * kBK * 4;
-    static constexpr int kStage = kABytes + kBK * kBN * 4;
-    // 1 KiB fetch blocks per wave and step: A has kBM / 8, B 16.
-    static constexpr int kFA = kBM / 8 / kWaves, kFB = 16 / kWaves;
+    static constexpr int kBRow = kBN * 4;  // bytes of one k row of B
+    static constexpr int kStage = kABytes + kBK * kBRow;
+    // 1 KiB fetch blocks per wave and step: A has kBM / 8, B kBK kBN / 256.
+    static constexpr int kBBlocks = kBK * kBRow / 1024;
+    static constexpr int kFA = kBM / 8 / kWaves, kFB = kBBlocks / kWaves;
     static constexpr int kFetch = kFA + kFB;
     static constexpr int kLds = kStages * kStage;
     static_assert((kBM / kWM) * kWavesN == kWaves, "waves tile the block");
-    static_assert(kFA * kWaves * 8 == kBM && kFB * kWaves == 16, "fetch blocks split evenly");
+    static_assert(kFA * kWaves * 8 == kBM && kFB * kWaves == kBBlocks, "fetch blocks split evenly");
+    static_assert(kBN == 128 || kBN == 256, "B rows of 512 or 1024 bytes");
+    static_assert(kBJ == 1 || kBJ == 2 || kBJ == 4, "column blocks per wave");
 };
 
-// The two configurations the library runs (mchip_f32_ring_plan picks one):
-// two blocks of 4 waves (64x64 quadrants) with 2 stages per CU, for products
-// with at least two tiles per CU, and one block of 8 waves (64x32) with 4
-// stages per CU otherwise.
-using McRingWide = McRingCfg<128, 64, 64, 4, 2>;
-using McRingDeep = McRingCfg<128, 64, 32, 8, 4>;
+// The configurations the library runs (mchip_f32_ring_plan picks one by a
+// cost model of the rounds each needs and its measured efficiency):
+//   big:  one block of 4 waves per CU, 256x256 tiles, 128x128 per wave (16
+//         accumulators, in AGPRs), 2 stages of 64 KiB;
+//   wide: two blocks of 4 waves per CU, 128x128 tiles, 64x64 per wave, 2
+//         stages;
+//   deep: one block of 4 waves per CU, 128x128 tiles, 64x64 per wave, 4
+//         stages (for fewer 128x128 tiles than two per CU).
+using McRingBig = McRingCfg<256, 256, 128, 128, 4, 2>;
+using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2>;
+using McRingDeep = McRingCfg<128, 128, 64, 64, 4, 4>;
 
 // LDS layout of a stage (bytes):
 //   A at 0: kBM / 8 blocks of 1 KiB, block rb holding rows 8 rb .. 8 rb + 7
@@ -57,9 +92,11 @@ using McRingDeep = McRingCfg<128, 64, 32, 8, 4>;
 //     An A-fragment read (32 lanes: 32 consecutive rows, one chunk) then
 //     puts every 16 lanes on 16 distinct 16-byte bank groups; a fetch
 //     instruction (lane l -> position l) still covers 8 whole 128-byte rows.
-//   B after A: k row kk at 512 kk, n-contiguous, its 16-byte chunk g stored
-//     at g ^ 8 (kk / 16 % 2), so the two half-waves of a read (k rows kk and
-//     kk + 16, the same 32 columns) use disjoint banks.
+//   B after A: k row kk at kBRow kk, n-contiguous, its 16-byte chunk g
+//     stored at g ^ 8 (kk / 16 % 2). The two half-waves of a read take k rows
+//     kk and kk + 16 and the same columns: with 4-byte reads the XOR puts
+//     them on disjoint banks; 8- and 16-byte reads stay contiguous within
+//     each half-wave (the XOR permutes within 256-byte windows).
 
 __device__ __forceinline__ int mc_ring_min(int a, int b) { return a < b ? a : b; }
 
@@ -77,7 +114,24 @@ struct McRingUnit {
 };
 
 // Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
-// 16 bytes at (LDS base + 16 l).
+// 16 bytes at (LDS base + 16 l). Instruction idx of a step's fetch: A
+// blocks first, then B blocks.
+template <class Cfg>
+__device__ __forceinline__ void mc_ring_fetch_one(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
+                                                  int t, int idx) {
+    if (idx < Cfg::kFA) {
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.a_src[idx] + t * Cfg::kBK),
+                                         reinterpret_cast<MC_RING_LDS void*>(wr + (wave * Cfg::kFA + idx) * 1024), 16, 0,
+                                         0);
+    } else {
+        const int i = idx - Cfg::kFA;
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(f.b_src[i] + t * f.b_step),
+            reinterpret_cast<MC_RING_LDS void*>(wr + Cfg::kABytes + (wave * Cfg::kFB + i) * 1024), 16, 0, 0);
+    }
+}
+
+// All of a step's fetch instructions (the prologue's).
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
                                               int t) {
@@ -96,34 +150,60 @@ __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, con
     }
 }
 
-// One step: optionally fetch a later step into `wr`, then multiply the step
-// held in `rd` (the MFMA sequence of the two-stage body). `rd` and `wr` are
-// distinct stages; declaring them __restrict__ gives the LDS reads alias
-// scopes that keep the compiler from making them wait for the fetch.
+// One step: multiply the step held in `rd` (the MFMA sequence of the
+// two-stage body) and, with do_fetch, fetch a later step into `wr`, its
+// instructions spread over the first 8 of the step's 16 MFMA groups. Issued
+// all at once, they stalled the wave in the memory pipe (each instruction
+// moves 1 KiB, and the CU's pipe takes a few tens of cycles per
+// instruction) while its matrix unit idled; spread, the pipe keeps up and
+// every fetch still has half a step to land. `rd` and `wr` are distinct
+// stages; declaring them __restrict__ gives the LDS reads alias scopes that
+// keep the compiler from making them wait for the fetch.
+//
+// The 16 groups (q, e) of a step each take one B read (and, at e = 0, the
+// K group's A reads). The reads of group t + 1 are issued before the MFMAs
+// of group t, into the other of two register sets, and a scheduling barrier
+// keeps them there: the MFMAs of group t then cover the LDS latency of group
+// t + 1 (left to itself the compiler reuses one register set and waits for
+// each read right before its MFMAs).
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __restrict__ rd,
                                              MC_RING_LDS unsigned char* __restrict__ wr, bool do_fetch,
                                              const McRingFetch<Cfg>& f, int wave, int fetch_t,
-                                             const int (&a_off)[Cfg::kAI][4], const int (&b_off)[Cfg::kBJ],
+                                             const int (&a_off)[Cfg::kAI][4], int b_off,
                                              mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ]) {
-    if (do_fetch) mc_ring_fetch<Cfg>(wr, f, wave, fetch_t);
+    typedef McRingVec<Cfg::kBJ> BV;
+    typedef typename BV::type BT;
+    mc_ring_f32x4 av[2][Cfg::kAI];
+    BT bv[2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        mc_ring_f32x4 av[Cfg::kAI];
+    for (int i = 0; i < Cfg::kAI; ++i) av[0][i] = *reinterpret_cast<const MC_RING_LDS mc_ring_f32x4*>(rd + a_off[i][0]);
+    bv[0] = *reinterpret_cast<const MC_RING_LDS BT*>(rd + b_off);
 #pragma unroll
-        for (int i = 0; i < Cfg::kAI; ++i) av[i] = *reinterpret_cast<const MC_RING_LDS mc_ring_f32x4*>(rd + a_off[i][q]);
+    for (int t = 0; t < 16; ++t) {
+        const int q = t >> 2, e = t & 3;
+        if (do_fetch) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float bv[Cfg::kBJ];
+            for (int idx = 0; idx < Cfg::kFetch; ++idx) {
+                if (idx * 8 / Cfg::kFetch == t) mc_ring_fetch_one<Cfg>(wr, f, wave, fetch_t, idx);
+            }
+        }
+        if (t + 1 < 16) {
+            if (((t + 1) & 3) == 0) {
+#pragma unroll
+                for (int i = 0; i < Cfg::kAI; ++i)
+                    av[(q + 1) & 1][i] = *reinterpret_cast<const MC_RING_LDS mc_ring_f32x4*>(rd + a_off[i][q + 1]);
+            }
+            bv[(t + 1) & 1] = *reinterpret_cast<const MC_RING_LDS BT*>(rd + b_off + (t + 1) * Cfg::kBRow);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < Cfg::kAI; ++i)
 #pragma unroll
             for (int j = 0; j < Cfg::kBJ; ++j)
-                bv[j] = *reinterpret_cast<const MC_RING_LDS float*>(rd + b_off[j] + (q * 4 + e) * 512);
-#pragma unroll
-            for (int i = 0; i < Cfg::kAI; ++i)
-#pragma unroll
-                for (int j = 0; j < Cfg::kBJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][e], bv[j], acc[i][j], 0, 0, 0);
-        }
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q & 1][i][e], BV::get(bv[t & 1], j), acc[i][j], 0,
+                                                                 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -154,6 +234,7 @@ template <class Cfg, typename Epilogue>
 __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, const float* __restrict__ b,
                                                  float* __restrict__ c, int m, int n, int k, int k_split, int splits,
                                                  float* __restrict__ partial, const Epilogue& epilogue) {
+    typedef McRingVec<Cfg::kBJ> BV;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[Cfg::kLds];
     MC_RING_LDS unsigned char* lds = (MC_RING_LDS unsigned char*)(smem);  // generic -> LDS address space
 
@@ -192,8 +273,10 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
     };
     // A: wave w fills blocks rb = kFA w + i; lane l -> row 8 rb + l % 8,
     // chunk 2 (l / 16) + ((l / 8 % 2) ^ (rb % 2)). B: wave w fills blocks
-    // bb = kFB w + i, k rows 2 bb and 2 bb + 1; lane l -> k row 2 bb + l / 32,
-    // logical chunk (l % 32) ^ 8 (k row / 16 % 2).
+    // bb = kFB w + i, each 1024 / kBRow k rows; lane l -> k row
+    // bb 1024 / kBRow + l / (kBRow / 16), physical chunk l % (kBRow / 16),
+    // logical chunk that ^ 8 (k row / 16 % 2).
+    constexpr int kLanesPerBRow = Cfg::kBRow / 16;
     auto fetch_of = [&](const McRingUnit& u) {
         McRingFetch<Cfg> f;
 #pragma unroll
@@ -205,8 +288,8 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
         }
 #pragma unroll
         for (int i = 0; i < Cfg::kFB; ++i) {
-            const int kk = 2 * (Cfg::kFB * wave + i) + (lane >> 5);
-            const int g = (lane & 31) ^ (8 * ((kk >> 4) & 1));
+            const int kk = (Cfg::kFB * wave + i) * (1024 / Cfg::kBRow) + lane / kLanesPerBRow;
+            const int g = (lane % kLanesPerBRow) ^ (8 * ((kk >> 4) & 1));
             const int col = mc_ring_min(u.col0 + 4 * g, n - 4);
             f.b_src[i] = b + static_cast<long long>(u.kb + kk) * n + col;
         }
@@ -215,8 +298,8 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
     };
 
     // Read offsets. Wave (wm, wn) owns rows kWM wm .. and columns kWN wn ..;
-    // lane l reads A rows wr + 32 i + l % 32 and B columns wc + 32 j + l % 32,
-    // k slot l / 32.
+    // lane l reads A rows wr + 32 i + l % 32 and B columns
+    // wc + kBJ (l % 32) .. + kBJ - 1, k slot l / 32.
     const int wr = (wave / Cfg::kWavesN) * Cfg::kWM, wc = (wave % Cfg::kWavesN) * Cfg::kWN;
     const int half = lane >> 5, li = lane & 31;
     int a_off[Cfg::kAI][4];
@@ -230,12 +313,8 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
             a_off[i][q] = rb * 1024 + 16 * (16 * (ch >> 1) + 8 * ((ch & 1) ^ (rb & 1)) + (row & 7));
         }
     }
-    int b_off[Cfg::kBJ];
-#pragma unroll
-    for (int j = 0; j < Cfg::kBJ; ++j) {
-        const int bcol = wc + 32 * j + li;
-        b_off[j] = Cfg::kABytes + half * 16 * 512 + (((bcol >> 2) ^ (8 * half)) << 4) + (bcol & 3) * 4;
-    }
+    const int lcol = wc + Cfg::kBJ * li;  // first of this lane's columns in the tile
+    const int b_off = Cfg::kABytes + half * 16 * Cfg::kBRow + (((lcol >> 2) ^ (8 * half)) << 4) + (lcol & 3) * 4;
 
     // Total steps of this block, and the fetch cursor (unit fi, step ft).
     int total = 0;
@@ -298,21 +377,25 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
         }
 
         // acc[i][j] value v of lane l: row wr + 32 i + 8 (v / 4) + 4 (l / 32) + v % 4,
-        // column wc + 32 j + l % 32.
+        // column lcol + j. The kBJ columns of a lane are stored together: with
+        // N a multiple of 4 they are all inside C or all past its edge.
+        const int col = u.col0 + lcol;
+        if (col >= n) continue;
         float* __restrict__ out = splits > 1 ? partial + static_cast<long long>(u.split) * m * n : c;
 #pragma unroll
-        for (int j = 0; j < Cfg::kBJ; ++j) {
-            const int col = u.col0 + wc + 32 * j + li;
-            if (col >= n) continue;
+        for (int i = 0; i < Cfg::kAI; ++i) {
 #pragma unroll
-            for (int i = 0; i < Cfg::kAI; ++i) {
+            for (int v = 0; v < 16; ++v) {
+                const int row = u.row0 + wr + 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
+                if (row >= m) continue;
+                const long long at = static_cast<long long>(row) * n + col;
+                typename BV::type o;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int row = u.row0 + wr + 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (row >= m) continue;
-                    const long long at = static_cast<long long>(row) * n + col;
-                    out[at] = splits > 1 ? acc[i][j][v] : epilogue(acc[i][j][v], static_cast<unsigned>(at));
+                for (int j = 0; j < Cfg::kBJ; ++j) {
+                    const float x = acc[i][j][v];
+                    BV::set(o, j, splits > 1 ? x : epilogue(x, static_cast<unsigned>(at + j)));
                 }
+                *reinterpret_cast<typename BV::type*>(out + at) = o;
             }
         }
     }

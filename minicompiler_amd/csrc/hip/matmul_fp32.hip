@@ -15,9 +15,10 @@
 //
 // double_buffered and split_k run the ring body (gemm_f32_ring.h) where the
 // shape allows: direct global -> LDS loads, persistent blocks walking their
-// tiles (and K splits) with an XCD-aware order, two stages and two blocks per
-// CU when there are enough tiles, else four stages and one 8-wave block per
-// CU. Its arithmetic is the two-stage body's, bit for bit.
+// tiles (and K splits) with an XCD-aware order, in one of three
+// configurations (256x256 tiles; 128x128 tiles with two blocks per CU; or
+// 128x128 tiles with four stages). Its arithmetic is the two-stage body's,
+// bit for bit.
 
 #include "matmul.h"
 
@@ -154,6 +155,7 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
     mc_gemm_f32_mfma<kDouble, kVec>(a, b, c, m, n, k, k_split, partial, McGemmStore{});
 }
 
+using RingBig = McRingBig;
 using RingWide = McRingWide;
 using RingDeep = McRingDeep;
 constexpr int kRBKRing = RingWide::kBK;
@@ -219,9 +221,13 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     const bool vec = n % 4 == 0 && k % 4 == 0 && aligned16(a) && aligned16(b);
     float* out_ws = depth > 1 ? workspace : nullptr;
     unsigned ring_grid = 0, ring_block = 0;
-    const int ring = double_buffer && vec ? mchip_f32_ring_plan(m, n, k, depth, device_cu_count(), &ring_grid, &ring_block)
-                                          : MCHIP_RING_NONE;
-    if (ring == MCHIP_RING_WIDE) {
+    const int ring = double_buffer && vec && aligned16(c)
+                         ? mchip_f32_ring_plan(m, n, k, depth, device_cu_count(), &ring_grid, &ring_block)
+                         : MCHIP_RING_NONE;
+    if (ring == MCHIP_RING_BIG) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingBig, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws);
+    } else if (ring == MCHIP_RING_WIDE) {
         hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws);
     } else if (ring == MCHIP_RING_DEEP) {
@@ -253,13 +259,28 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     if (m < 1 || n < 4 || k < kRBKRing || k % kRBKRing != 0 || n % 4 != 0 || depth < 1 || cu_count < 1) {
         return MCHIP_RING_NONE;
     }
-    const long long units = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
-    if (units >= 2LL * cu_count) {
-        *grid = static_cast<unsigned>(2 * cu_count);
+    // Time in units of one 128x128 tile-split on a whole CU: rounds of
+    // tile-splits per block slot x work per tile-split (a 256x256 tile is
+    // four; two blocks sharing a CU each run at half speed) / efficiency
+    // (measured on 8192^3, 4096^3 and the MLP shapes: about 0.92, 0.86 and
+    // 0.80 of the matrix peak inside the main loop).
+    const long long cus = cu_count;
+    const long long t256 = static_cast<long long>((m + 255) / 256) * ((n + 255) / 256) * depth;
+    const long long t128 = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
+    const double big = static_cast<double>((t256 + cus - 1) / cus) * 4.0 / 0.92;
+    const double wide = static_cast<double>((t128 + 2 * cus - 1) / (2 * cus)) * 2.0 / 0.86;
+    const double deep = static_cast<double>((t128 + cus - 1) / cus) * 1.0 / 0.80;
+    if (big <= wide && big <= deep) {
+        *grid = static_cast<unsigned>(std::min(t256, cus));
+        *block = RingBig::kThreads;
+        return MCHIP_RING_BIG;
+    }
+    if (wide <= deep) {
+        *grid = static_cast<unsigned>(std::min(t128, 2 * cus));
         *block = RingWide::kThreads;
         return MCHIP_RING_WIDE;
     }
-    *grid = static_cast<unsigned>(std::min<long long>(units, cu_count));
+    *grid = static_cast<unsigned>(std::min(t128, cus));
     *block = RingDeep::kThreads;
     return MCHIP_RING_DEEP;
 }

@@ -132,8 +132,8 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
             "launch_reps": reps}
 
 
-def bench_mlp(mc, batch: int, steps: int, warmup: int) -> dict:
-    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch})
+def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None) -> dict:
+    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
     t = time_graph(mc, c, steps, warmup)
@@ -334,6 +334,19 @@ def main() -> int:
                          "config": {"workload": k["config"], **k["dims"]},
                          "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
+    if args.workload == "mlp" and not args.quick:
+        # BASELINE config 2's batch sweep: the small batches are launch-bound,
+        # so each is timed with direct launches and with hipGraph replay.
+        cfgs = line.setdefault("configs", {})
+        for b in (256, 1024):
+            entry = {}
+            for mode, opts in (("direct", None), ("graph_replay", {"graph": 1})):
+                r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts)
+                entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
+                               "launches": r["compiled"].kernel_launches}
+            cfgs[f"mlp_b{b}"] = entry
+            log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
+                f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step")
     if args.workload == "gemm_fp32" or (args.workload == "mlp" and not args.quick):
         shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384), (16, 4096, 4096)]
         g = bench_gemm_fp32(mc, cus, shapes, 10, 3)

@@ -24,9 +24,12 @@ namespace minicompiler::hip {
 //     8x8 / 4x4 register block per lane).
 //   Vectorized: 128x128 tiles staged in LDS with 16-byte global loads, the
 //     products on the FP32 matrix cores (v_mfma_f32_32x32x2_f32), one LDS stage.
-//   DoubleBuffered: Vectorized with two LDS stages; the next tile's global
-//     loads are in flight while the current one is multiplied.
-//   SplitK: DoubleBuffered with K split over the grid's depth and a
+//   DoubleBuffered: Vectorized with the next tile's loads in flight while
+//     the current one is multiplied: where K % 32 = 0 and N % 4 = 0, a ring
+//     of 2 or 4 LDS stages filled by direct global -> LDS loads, persistent
+//     blocks in XCD order, 256x256 or 128x128 tiles; otherwise two LDS
+//     stages. The same arithmetic as Vectorized, bit for bit.
+//   SplitK: DoubleBuffered with K split into whole 32-wide steps and a
 //     deterministic fixed-order reduction of the partial products.
 //   TensorCoreBf16 / TensorCoreF16: inputs rounded to nearest-even into
 //     bf16 / fp16 while they are staged in LDS, products on the bf16 / fp16
@@ -81,6 +84,14 @@ struct HipOptions {
     // results match that kernel bit for bit. Off: the staging kernel rounds
     // while it stages (and splits K where SplitK would).
     bool convert_tensor_core_operands = true;
+    // enqueue() captures its launches into a HIP graph the first time and
+    // replays that graph afterwards (one submission instead of one per
+    // kernel); binding other buffers captures again. The graph holds kernel
+    // launches and, for graph outputs that are inputs or constants, copies;
+    // no memsets. The stream must be one that can be captured (not the
+    // legacy null stream). enqueue_launch and enqueue_with_events launch
+    // directly.
+    bool graph_replay = false;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).

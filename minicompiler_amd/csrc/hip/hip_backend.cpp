@@ -107,6 +107,7 @@ public:
         : graph_(graph), options_(options), plan_(plan_memory(graph_)) {}
 
     ~HipExecutableImpl() override {
+        drop_graph();
         if (stream_) mchip_stream_destroy(stream_);
         if (arena_) mchip_free(arena_);
     }
@@ -270,7 +271,24 @@ public:
         return Status();
     }
 
-    Status enqueue(void* stream) override { return enqueue_with_events(stream, nullptr); }
+    Status enqueue(void* stream) override {
+        if (!options_.graph_replay) return enqueue_with_events(stream, nullptr);
+        void* s = stream ? stream : stream_;
+        if (graph_exec_ == nullptr) {
+            MCHIP_TRY(mchip_capture_begin(s));
+            Status st = enqueue_with_events(s, nullptr);
+            void* exec = nullptr;
+            const int rc = mchip_capture_end(s, &exec);  // ends the capture also after a failed launch
+            if (!st.ok()) {
+                if (exec) mchip_graph_exec_destroy(exec);
+                return st;
+            }
+            if (rc != 0) return hip_status(rc, "hipStreamEndCapture / hipGraphInstantiate");
+            graph_exec_ = exec;
+        }
+        MCHIP_TRY(mchip_graph_launch(graph_exec_, s));
+        return Status();
+    }
 
     Status enqueue_with_events(void* stream, void* const* events) override {
         void* s = stream ? stream : stream_;
@@ -323,6 +341,7 @@ public:
             bound_[static_cast<std::size_t>(graph_.inputs()[k])] = const_cast<void*>(device_inputs[k]);
         }
         refresh_pointers();
+        drop_graph();
         return Status();
     }
 
@@ -337,6 +356,7 @@ public:
             if (is_compute(graph_.node(id).op)) bound_[static_cast<std::size_t>(id)] = device_outputs[k];
         }
         refresh_pointers();
+        drop_graph();
         return Status();
     }
 
@@ -435,6 +455,12 @@ private:
             return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " + mchip_error_string(rc)};
         }
         return Status();
+    }
+
+    // The captured graph holds the kernel arguments of the time of capture.
+    void drop_graph() {
+        if (graph_exec_) mchip_graph_exec_destroy(graph_exec_);
+        graph_exec_ = nullptr;
     }
 
     NodeId a_of(const Launch& l) const { return graph_.node(l.node).inputs[0]; }
@@ -691,6 +717,7 @@ private:
     MemoryPlan plan_;
     DeviceInfo device_;
     void* stream_ = nullptr;
+    void* graph_exec_ = nullptr;  // graph_replay: the captured enqueue
     void* arena_ = nullptr;
     std::size_t arena_bytes_ = 0;
     std::vector<std::size_t> offset_;    // per node: arena offset

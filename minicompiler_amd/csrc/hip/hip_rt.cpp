@@ -137,4 +137,24 @@ int mchip_occupancy(int* blocks_per_cu, void* function, int block, size_t shared
                                                               block, shared_bytes);
 }
 
+int mchip_capture_begin(void* stream) {
+    return hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal);
+}
+int mchip_capture_end(void* stream, void** exec) {
+    *exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph);
+    if (e != hipSuccess) return e;
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return e;
+    *exec = x;
+    return hipSuccess;
+}
+int mchip_graph_launch(void* exec, void* stream) {
+    return hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(stream));
+}
+int mchip_graph_exec_destroy(void* exec) { return hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)); }
+
 }  // extern "C"

@@ -74,6 +74,15 @@ int mchip_module_launch3(void* function, unsigned grid_x, unsigned grid_y, unsig
                          unsigned shared_bytes, void* stream, void** params);
 int mchip_occupancy(int* blocks_per_cu, void* function, int block, size_t shared_bytes);
 
+/* Stream capture and replay: hipStreamBeginCapture (thread-local mode);
+ * hipStreamEndCapture then hipGraphInstantiate, giving *exec (the graph
+ * itself is released; on failure *exec is NULL and capture has ended);
+ * hipGraphLaunch; hipGraphExecDestroy. */
+int mchip_capture_begin(void* stream);
+int mchip_capture_end(void* stream, void** exec);
+int mchip_graph_launch(void* exec, void* stream);
+int mchip_graph_exec_destroy(void* exec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,40 @@
+"""hipGraph replay of enqueue (option graph=1): the first enqueue captures
+the executable's launches into a graph, later ones replay it. Each replay,
+with eager uploads and synchronisations between replays, must equal an
+executable that launches directly, bit for bit; binding other buffers
+captures again. (The reference runs graphs only around its GEMM timing,
+bench/bench_cuda.cpp:445-493; replaying a whole enqueue is this build's.)"""
+
+import numpy as np
+import pytest
+
+from helpers import uniform_inputs
+
+pytestmark = pytest.mark.gpu
+
+CASES = [("mlp_gelu", {"B": 256}, {}), ("mlp_gelu", {"B": 256}, {"matmul": "tensor_core_bf16"}),
+         ("gelu_chain", {"M": 64, "N": 4096}, {}), ("batchnorm_relu", {"R": 512, "C": 256}, {})]
+
+
+@pytest.mark.parametrize("name,dims,opts", CASES)
+def test_every_graph_replay_equals_direct_launches(device, mc, oracle, name, dims, opts):
+    print(f"case graph {name} {dims} {opts}", flush=True)
+    direct = mc.Compiled(path=mc.graph_path(name), dims=dims, options=opts)
+    replay = mc.Compiled(path=mc.graph_path(name), dims=dims, options={**opts, "graph": 1})
+    want = None
+    for rep in range(4):
+        inputs = uniform_inputs(oracle, direct.input_sizes, 10 + rep)
+        want = direct.run(inputs)  # eager work between the replays
+        replay.upload(inputs)
+        replay.enqueue()  # captures at rep 0, replays afterwards
+        got = replay.download()
+        for g, w in zip(got, want):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"replay {rep}"
+    # Binding an output buffer captures again; the replay writes it in place.
+    out = mc.DeviceBuffer(4 * replay.output_sizes[0])
+    out.fill_bytes(0xFF)
+    replay.bind_outputs([out.ptr] + [None] * (len(replay.output_sizes) - 1))
+    for _ in range(2):
+        replay.enqueue()
+        replay.synchronize()
+        assert np.array_equal(out.download().view(np.uint32), want[0].view(np.uint32))

@@ -80,10 +80,14 @@ struct McRingCfg {
 //   wide: two blocks of 4 waves per CU, 128x128 tiles, 64x64 per wave, 2
 //         stages;
 //   deep: one block of 4 waves per CU, 128x128 tiles, 64x64 per wave, 4
-//         stages (for fewer 128x128 tiles than two per CU).
+//         stages (for fewer 128x128 tiles than two per CU);
+//   thin: for M <= 32 (HBM-bound on B): 32x128 tiles, 4 waves of 32x32, 6
+//         stages of 20 KiB keeping more of B in flight, so a 128-row tile's
+//         MFMA work on clamped rows no longer dominates.
 using McRingBig = McRingCfg<256, 256, 128, 128, 4, 2>;
 using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2>;
 using McRingDeep = McRingCfg<128, 128, 64, 64, 4, 4>;
+using McRingThin = McRingCfg<32, 128, 32, 32, 4, 6>;
 
 // LDS layout of a stage (bytes):
 //   A at 0: kBM / 8 blocks of 1 KiB, block rb holding rows 8 rb .. 8 rb + 7
@@ -209,6 +213,21 @@ __device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __
 
 // s_waitcnt vmcnt(v) lgkmcnt(0), expcnt not waited on (gfx9 encoding).
 #define MC_RING_WAIT(v) __builtin_amdgcn_s_waitcnt(0x0070 | ((v) & 15) | (((v) >> 4) << 14))
+
+// Wait until at most `later` fetch groups of kFetch instructions are in
+// flight (later <= kMax, the ring's stages minus two), and for LDS reads.
+template <int kFetch, int kMax>
+__device__ __forceinline__ void mc_ring_wait_later(int later) {
+    if constexpr (kMax > 0) {
+        if (later >= kMax) {
+            MC_RING_WAIT(kMax * kFetch);
+            return;
+        }
+        mc_ring_wait_later<kFetch, kMax - 1>(later);
+    } else {
+        MC_RING_WAIT(0);
+    }
+}
 
 // A workgroup barrier without a memory fence; the compiler may not move
 // memory operations or MFMAs across it.
@@ -355,14 +374,7 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
             // Fetch groups issued after the one of step g (stores issued
             // after it only make the wait longer): wait for that one and for
             // this wave's LDS reads of the previous step.
-            const int later = issued - g - 1;
-            if (later >= 2) {
-                MC_RING_WAIT(2 * Cfg::kFetch);
-            } else if (later == 1) {
-                MC_RING_WAIT(Cfg::kFetch);
-            } else {
-                MC_RING_WAIT(0);
-            }
+            mc_ring_wait_later<Cfg::kFetch, Cfg::kStages - 2>(issued - g - 1);
             // Every wave's fetch of step g has landed, and every wave is done
             // with step g - 1, whose stage the next fetch overwrites.
             mc_ring_barrier();

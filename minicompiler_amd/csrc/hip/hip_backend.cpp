@@ -506,6 +506,7 @@ private:
         unsigned grid = 0, block = 0;
         switch (mchip_f32_ring_plan(l.m, l.n, l.k, l.depth, device_.cu_count, &grid, &block)) {
             case MCHIP_RING_BIG: return GemmBody::F32RingBig;
+            case MCHIP_RING_THIN: return GemmBody::F32RingThin;
             case MCHIP_RING_WIDE: return GemmBody::F32RingWide;
             case MCHIP_RING_DEEP: return GemmBody::F32RingDeep;
             default: return GemmBody::F32Mfma;

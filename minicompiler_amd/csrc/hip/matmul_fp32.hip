@@ -16,9 +16,9 @@
 // double_buffered and split_k run the ring body (gemm_f32_ring.h) where the
 // shape allows: direct global -> LDS loads, persistent blocks walking their
 // tiles (and K splits) with an XCD-aware order, in one of three
-// configurations (256x256 tiles; 128x128 tiles with two blocks per CU; or
-// 128x128 tiles with four stages). Its arithmetic is the two-stage body's,
-// bit for bit.
+// configurations (256x256 tiles; 128x128 tiles with two blocks per CU;
+// 128x128 tiles with four stages; 32x128 tiles for M <= 32). Its arithmetic
+// is the two-stage body's, bit for bit.
 
 #include "matmul.h"
 
@@ -158,6 +158,7 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
 using RingBig = McRingBig;
 using RingWide = McRingWide;
 using RingDeep = McRingDeep;
+using RingThin = McRingThin;
 constexpr int kRBKRing = RingWide::kBK;
 
 template <class Cfg, int kBlocksPerCu>
@@ -224,7 +225,10 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     const int ring = double_buffer && vec && aligned16(c)
                          ? mchip_f32_ring_plan(m, n, k, depth, device_cu_count(), &ring_grid, &ring_block)
                          : MCHIP_RING_NONE;
-    if (ring == MCHIP_RING_BIG) {
+    if (ring == MCHIP_RING_THIN) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingThin, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws);
+    } else if (ring == MCHIP_RING_BIG) {
         hipLaunchKernelGGL((matmul_ring_f32<RingBig, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws);
     } else if (ring == MCHIP_RING_WIDE) {
@@ -265,6 +269,12 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     // (measured on 8192^3, 4096^3 and the MLP shapes: about 0.92, 0.86 and
     // 0.80 of the matrix peak inside the main loop).
     const long long cus = cu_count;
+    if (m <= RingThin::kBM) {
+        const long long t32 = static_cast<long long>((n + 127) / 128) * depth;
+        *grid = static_cast<unsigned>(std::min(t32, cus));
+        *block = RingThin::kThreads;
+        return MCHIP_RING_THIN;
+    }
     const long long t256 = static_cast<long long>((m + 255) / 256) * ((n + 255) / 256) * depth;
     const long long t128 = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
     const double big = static_cast<double>((t256 + cus - 1) / cus) * 4.0 / 0.92;

@@ -24,9 +24,10 @@ GUARD = 4096  # floats after C, prefilled with NaN; must stay untouched
 # two 128x128 blocks per CU, ragged (512 tiles); the same with some CUs
 # holding one block (304 tiles); one 4-stage block per CU with a grid of 9
 # (not a multiple of 8) and with 256 tiles (the class of the MLP's second
-# GEMM); one row, one K step.
+# GEMM); one row, one K step; M <= 32 (32x128 tiles, 6 stages), N ragged and
+# a grid of 33, and a single tile.
 SHAPES = [(4000, 64, 4000), (4096, 32, 8192), (4000, 64, 2000), (2048, 96, 2432), (300, 96, 260), (8192, 256, 512),
-          (1, 32, 4)]
+          (1, 32, 4), (16, 1024, 4100), (32, 64, 256)]
 
 
 def run(mc, kernel, da, db, m, n, k):

@@ -114,6 +114,7 @@ int mchip_rtc_compile(const char* source, const char* file_name, const char* con
 }
 
 void mchip_rtc_free(void* p) { std::free(p); }
+int mchip_rtc_version(int* major, int* minor) { return hiprtcVersion(major, minor); }
 
 int mchip_module_load(void** module, const void* image) {
     return hipModuleLoadData(reinterpret_cast<hipModule_t*>(module), image);

@@ -64,6 +64,8 @@ const char* mchip_rtc_error_string(int code);
 int mchip_rtc_compile(const char* source, const char* file_name, const char* const* options, int num_options,
                       char** code, size_t* code_size, char** log);
 void mchip_rtc_free(void* p);
+/* hiprtcVersion. */
+int mchip_rtc_version(int* major, int* minor);
 
 int mchip_module_load(void** module, const void* image);
 int mchip_module_unload(void* module);

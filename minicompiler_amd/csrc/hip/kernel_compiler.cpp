@@ -39,6 +39,29 @@ bool read_file(const std::string& path, std::string* out) {
     return !out->empty();
 }
 
+// A cache file: the magic line, the key's length in decimal and a newline,
+// the key itself, then the code object. A file whose key differs from the
+// requested one (a hash collision, or a key from another compiler) is not
+// used.
+constexpr const char* kCacheMagic = "minicompiler-hip code object v1\n";
+
+std::string cache_file_contents(const std::string& key, const std::string& code) {
+    return std::string(kCacheMagic) + std::to_string(key.size()) + '\n' + key + code;
+}
+
+bool code_from_cache_file(const std::string& file, const std::string& key, std::string* code) {
+    const std::string magic(kCacheMagic);
+    if (file.compare(0, magic.size(), magic) != 0) return false;
+    const std::size_t nl = file.find('\n', magic.size());
+    if (nl == std::string::npos) return false;
+    const std::string len_text = file.substr(magic.size(), nl - magic.size());
+    if (len_text.empty() || len_text.find_first_not_of("0123456789") != std::string::npos) return false;
+    const std::size_t len = std::stoull(len_text);
+    if (len != key.size() || file.size() <= nl + 1 + len || file.compare(nl + 1, len, key) != 0) return false;
+    *code = file.substr(nl + 1 + len);
+    return true;
+}
+
 void write_file_atomically(const std::string& path, const std::string& data) {
     const std::string tmp = path + ".tmp" + std::to_string(reinterpret_cast<std::uintptr_t>(&data));
     {
@@ -50,7 +73,9 @@ void write_file_atomically(const std::string& path, const std::string& data) {
 }
 
 std::string cache_key(const std::string& arch, const std::string& source) {
-    std::string key = arch;
+    int major = 0, minor = 0;
+    mchip_rtc_version(&major, &minor);
+    std::string key = "hiprtc " + std::to_string(major) + "." + std::to_string(minor) + '\n' + arch;
     for (const std::string& o : KernelCompiler::options_for(arch)) key += '\n' + o;
     return key + '\n' + source;
 }
@@ -73,7 +98,8 @@ Result<std::string> KernelCompiler::compile_code_object(const std::string& sourc
     const std::string key = cache_key(arch, source);
     const std::string path = disk_cache_path(key);
     std::string code;
-    if (!path.empty() && read_file(path, &code)) {
+    std::string file;
+    if (!path.empty() && read_file(path, &file) && code_from_cache_file(file, key, &code)) {
         if (compile_ms) *compile_ms = 0.0;
         return code;
     }
@@ -94,7 +120,7 @@ Result<std::string> KernelCompiler::compile_code_object(const std::string& sourc
     }
     code.assign(image, size);
     mchip_rtc_free(image);
-    if (!path.empty()) write_file_atomically(path, code);
+    if (!path.empty()) write_file_atomically(path, cache_file_contents(key, code));
     if (compile_ms) {
         *compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     }

@@ -8,7 +8,10 @@ pass over one batch of synthetic, seeded input already resident in HBM).
 The headline workload is BASELINE config 2, the fp32 MLP block
 (mlp_gelu.mcg) at B=8192: GEMM, fused bias+GELU, GEMM, fused
 bias+residual. W untimed steps, then exactly K timed steps between two HIP
-events on the executable's stream. Each kernel's duration is then measured
+events on the executable's stream (the default W = 300, about 100 ms at
+B=8192, brings the GPU to its steady clock: it raises the clock only under
+sustained load; every other configuration warms up for WARM_SECONDS of its
+own work). Each kernel's duration is then measured
 in the same process on the same stream: the launch alone, back to back,
 between one pair of HIP events (events between launches would add their own
 gaps to short kernels).
@@ -43,6 +46,9 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_BF16_TFLOPS = 2500.0
 METRIC = "fused-kernel HBM GB/s + GEMM TFLOPS, % of MI355X roofline, 1 GPU"
 MALL_BYTES = 256 << 20
+# Warm-up time of every configuration other than the headline step (which
+# runs exactly --warmup untimed steps).
+WARM_SECONDS = 0.3
 
 
 def log(msg: str) -> None:
@@ -86,13 +92,28 @@ def rate_entry(name: str, work: dict, ms: float, gemm_peak: float = PEAK_FP32_TF
             "frac": gbs / PEAK_HBM_GBS}
 
 
-def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None) -> dict:
-    """W warmup steps, then K steps timed between one pair of HIP events on
-    the executable's stream (ms_per_step). Then each launch of the step alone,
-    `reps` times back to back between one pair of HIP events on that stream
-    (its mean duration, with no event between launches to perturb it).
-    `rotations`: list of (input_ptrs, output_ptrs) bound in turn, so
-    consecutive launches touch different buffers (defeats the 256 MB MALL)."""
+def warm_up_for(seconds: float, batch) -> int:
+    """Calls `batch()` (some launches, then a wait for them) until `seconds`
+    have passed; returns the number of calls. The GPU raises its clock only
+    under sustained load (about 35 ms of back-to-back GEMMs on an MI355X to
+    reach a steady clock), so the configurations below warm up for a time,
+    as the reference's bench does (bench/bench_cuda.cpp:124-130)."""
+    calls, until = 0, time.perf_counter() + seconds
+    while time.perf_counter() < until:
+        batch()
+        calls += 1
+    return calls
+
+
+def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None,
+               warm_seconds: float = 0.0) -> dict:
+    """W warmup steps (then more until `warm_seconds` have passed), then K
+    steps timed between one pair of HIP events on the executable's stream
+    (ms_per_step). Then each launch of the step alone, `reps` times back to
+    back between one pair of HIP events on that stream (its mean duration,
+    with no event between launches to perturb it). `rotations`: list of
+    (input_ptrs, output_ptrs) bound in turn, so consecutive launches touch
+    different buffers (defeats the 256 MB MALL)."""
     def bind(i):
         if rotations:
             ins, outs = rotations[i % len(rotations)]
@@ -104,6 +125,14 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
         bind(i)
         compiled.enqueue()
     compiled.synchronize()
+
+    def extra():
+        for i in range(max(warmup, 10)):
+            bind(i)
+            compiled.enqueue()
+        compiled.synchronize()
+
+    warm_up_for(warm_seconds, extra)
     start, stop = mc.Event(), mc.Event()
     t0 = time.perf_counter()
     start.record(stream)
@@ -132,11 +161,11 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
             "launch_reps": reps}
 
 
-def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None) -> dict:
+def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0) -> dict:
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
-    t = time_graph(mc, c, steps, warmup)
+    t = time_graph(mc, c, steps, warmup, warm_seconds=warm_seconds)
     work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
@@ -158,7 +187,7 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
         bi, bo = mc.DeviceBuffer.from_array(x), mc.DeviceBuffer(4 * n_out)
         bufs.append((bi, bo))
     rot = [([bi.ptr], [bo.ptr]) for bi, bo in bufs]
-    t = time_graph(mc, c, steps, warmup, rot)
+    t = time_graph(mc, c, steps, warmup, rot, warm_seconds=WARM_SECONDS)
     work = node_work(c.graph(), c.launch_nodes)
     (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
     return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
@@ -167,10 +196,18 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
 
 def time_gemm(mc, launch, steps: int, warmup: int) -> float:
     """Mean duration of `steps` back-to-back launches between one pair of HIP
-    events on their stream."""
+    events on their stream, after `warmup` launches and a warm-up of
+    WARM_SECONDS."""
     s = mc.Stream()
     for _ in range(warmup):
         launch(s)
+
+    def extra():
+        for _ in range(4):
+            launch(s)
+        s.synchronize()
+
+    warm_up_for(WARM_SECONDS, extra)
     start, stop = mc.Event(), mc.Event()
     start.record(s)
     for _ in range(steps):
@@ -266,8 +303,10 @@ def measured_traffic(workload: str, launch: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # About 70 ms of timed work at B=8192; the 300 warmup steps (about 100 ms)
+    # bring the GPU to its steady clock first.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="mlp",
                     choices=["mlp", "gelu", "batchnorm", "gemm_fp32", "gemm_bf16", "copy"])
     ap.add_argument("--batch", type=int, default=8192)
@@ -341,7 +380,7 @@ def main() -> int:
         for b in (256, 1024):
             entry = {}
             for mode, opts in (("direct", None), ("graph_replay", {"graph": 1})):
-                r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts)
+                r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts, WARM_SECONDS)
                 entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
                                "launches": r["compiled"].kernel_launches}
             cfgs[f"mlp_b{b}"] = entry
@@ -349,7 +388,7 @@ def main() -> int:
                 f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step")
     if args.workload == "gemm_fp32" or (args.workload == "mlp" and not args.quick):
         shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384), (16, 4096, 4096)]
-        g = bench_gemm_fp32(mc, cus, shapes, 10, 3)
+        g = bench_gemm_fp32(mc, cus, shapes, 10, 3)  # plus WARM_SECONDS per shape
         line.setdefault("configs", {})["gemm_fp32"] = g
         if args.workload == "gemm_fp32":
             top = g[2]
@@ -358,7 +397,7 @@ def main() -> int:
                          "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
                                       "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
     if args.workload == "gemm_bf16" or (args.workload == "mlp" and not args.quick):
-        g = bench_gemm_lowp(mc, [(8192, 8192, 8192), (4096, 14336, 4096)], 10, 3)
+        g = bench_gemm_lowp(mc, [(8192, 8192, 8192), (4096, 14336, 4096)], 20, 3)  # plus WARM_SECONDS
         line.setdefault("configs", {})["gemm_bf16_fp16"] = g
         if args.workload == "gemm_bf16":
             top = g[0]

@@ -208,8 +208,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         return {os.str()};
     }
     const char* bounds =
-        body == GemmBody::F32RingBig || body == GemmBody::F32RingDeep || body == GemmBody::F32RingThin ? "256, 1"
-                                                                                                         : "256, 2";
+        body == GemmBody::F32RingBig || body == GemmBody::F32RingThin ? "256, 1" : "256, 2";
     os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
           "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n"
@@ -219,7 +218,6 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
            << ", " << (constant ? std::to_string(fixed.k_split) : std::string("k_split")) << ", partial, epi);\n}\n\n";
     } else {
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"
-                          : body == GemmBody::F32RingDeep ? "McRingDeep"
                           : body == GemmBody::F32RingThin ? "McRingThin"
                                                           : "McRingWide";
         os << "\tmc_gemm_f32_ring<" << cfg << ">(a, b, c, "

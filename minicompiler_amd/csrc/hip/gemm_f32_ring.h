@@ -52,8 +52,11 @@ struct McRingVec<4> {
 // 16-byte LDS read gives a lane the B values of all its column blocks, and C
 // is stored kBJ floats at a time. The MFMA sequence of each C element does
 // not depend on this assignment.
-template <int kBM_, int kBN_, int kWM_, int kWN_, int kWaves_, int kStages_>
+template <int kBM_, int kBN_, int kWM_, int kWN_, int kWaves_, int kStages_, bool kStaged_ = false>
 struct McRingCfg {
+    // kStaged: the fetch goes through registers (a 16-byte global load one
+    // step ahead, written to LDS the next step) instead of direct loads.
+    static constexpr bool kStaged = kStaged_;
     static constexpr int kBM = kBM_, kBN = kBN_, kBK = 32;
     static constexpr int kWM = kWM_, kWN = kWN_, kWaves = kWaves_, kStages = kStages_;
     static constexpr int kThreads = kWaves * 64;
@@ -76,17 +79,18 @@ struct McRingCfg {
 // The configurations the library runs (mchip_f32_ring_plan picks one by a
 // cost model of the rounds each needs and its measured efficiency):
 //   big:  one block of 4 waves per CU, 256x256 tiles, 128x128 per wave (16
-//         accumulators, in AGPRs), 2 stages of 64 KiB;
-//   wide: two blocks of 4 waves per CU, 128x128 tiles, 64x64 per wave, 2
-//         stages;
-//   deep: one block of 4 waves per CU, 128x128 tiles, 64x64 per wave, 4
-//         stages (for fewer 128x128 tiles than two per CU);
+//         accumulators, in AGPRs), 2 stages of 64 KiB, direct fetch;
+//   wide: up to two blocks of 4 waves per CU, 128x128 tiles, 64x64 per wave
+//         (accumulators in VGPRs), 2 stages, fetch staged through registers
+//         a step ahead (measured 3-7% faster than its direct-fetch form, and
+//         than a 4-stage direct-fetch form with one block per CU, on every
+//         shape it is chosen for; with one block of 4 waves per SIMD set a
+//         direct fetch instruction holds up the wave's MFMA issue);
 //   thin: for M <= 32 (HBM-bound on B): 32x128 tiles, 4 waves of 32x32, 6
 //         stages of 20 KiB keeping more of B in flight, so a 128-row tile's
 //         MFMA work on clamped rows no longer dominates.
 using McRingBig = McRingCfg<256, 256, 128, 128, 4, 2>;
-using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2>;
-using McRingDeep = McRingCfg<128, 128, 64, 64, 4, 4>;
+using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2, true>;
 using McRingThin = McRingCfg<32, 128, 32, 32, 4, 6>;
 
 // LDS layout of a stage (bytes):
@@ -135,6 +139,23 @@ __device__ __forceinline__ void mc_ring_fetch_one(MC_RING_LDS unsigned char* wr,
     }
 }
 
+// The staged fetch: instruction idx of a step as a 16-byte global load into
+// registers, and later the store of those registers to the LDS position the
+// direct load would fill (so both fetch forms give the same stage contents).
+template <class Cfg>
+__device__ __forceinline__ mc_ring_f32x4 mc_ring_load_one(const McRingFetch<Cfg>& f, int t, int idx) {
+    if (idx < Cfg::kFA) return *reinterpret_cast<const mc_ring_f32x4*>(f.a_src[idx] + t * Cfg::kBK);
+    return *reinterpret_cast<const mc_ring_f32x4*>(f.b_src[idx - Cfg::kFA] + t * f.b_step);
+}
+
+template <class Cfg>
+__device__ __forceinline__ void mc_ring_store_one(MC_RING_LDS unsigned char* wr, int wave, int lane, int idx,
+                                                  mc_ring_f32x4 v) {
+    const int blk = idx < Cfg::kFA ? (wave * Cfg::kFA + idx) * 1024
+                                   : Cfg::kABytes + (wave * Cfg::kFB + idx - Cfg::kFA) * 1024;
+    *reinterpret_cast<MC_RING_LDS mc_ring_f32x4*>(wr + blk + 16 * lane) = v;
+}
+
 // All of a step's fetch instructions (the prologue's).
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
@@ -170,12 +191,20 @@ __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, con
 // keeps them there: the MFMAs of group t then cover the LDS latency of group
 // t + 1 (left to itself the compiler reuses one register set and waits for
 // each read right before its MFMAs).
+//
+// Staged configurations: the registers loaded one step ago are written to
+// `wr`, and the next fetch is loaded into the same registers right behind
+// each write, so every load has a whole step to land. Both happen at every
+// step (past the last step they move data no step reads, into a stage no
+// later step reads): with either one conditional, the compiler's wait before
+// each write would also wait for this step's loads.
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __restrict__ rd,
                                              MC_RING_LDS unsigned char* __restrict__ wr, bool do_fetch,
                                              const McRingFetch<Cfg>& f, int wave, int fetch_t,
                                              const int (&a_off)[Cfg::kAI][4], int b_off,
-                                             mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ]) {
+                                             mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ],
+                                             mc_ring_f32x4 (&staged)[Cfg::kFetch]) {
     typedef McRingVec<Cfg::kBJ> BV;
     typedef typename BV::type BT;
     mc_ring_f32x4 av[2][Cfg::kAI];
@@ -186,7 +215,16 @@ __device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
         const int q = t >> 2, e = t & 3;
-        if (do_fetch) {
+        if constexpr (Cfg::kStaged) {
+            const int lane = static_cast<int>(threadIdx.x) & 63;
+#pragma unroll
+            for (int idx = 0; idx < Cfg::kFetch; ++idx) {
+                if (idx * 8 / Cfg::kFetch == t) {
+                    mc_ring_store_one<Cfg>(wr, wave, lane, idx, staged[idx]);
+                    staged[idx] = mc_ring_load_one<Cfg>(f, fetch_t, idx);
+                }
+            }
+        } else if (do_fetch) {
 #pragma unroll
             for (int idx = 0; idx < Cfg::kFetch; ++idx) {
                 if (idx * 8 / Cfg::kFetch == t) mc_ring_fetch_one<Cfg>(wr, f, wave, fetch_t, idx);
@@ -229,6 +267,22 @@ __device__ __forceinline__ void mc_ring_wait_later(int later) {
     }
 }
 
+// Staged configurations: wait until the prologue's direct fetch of step g
+// has landed, `later` = direct fetch groups issued after it (one group of
+// staged loads, issued after all of them, is always in flight too).
+template <int kFetch, int kMax>
+__device__ __forceinline__ void mc_ring_wait_direct(int later) {
+    if constexpr (kMax > 0) {
+        if (later >= kMax) {
+            MC_RING_WAIT((kMax + 1) * kFetch);
+            return;
+        }
+        mc_ring_wait_direct<kFetch, kMax - 1>(later);
+    } else {
+        MC_RING_WAIT(kFetch);
+    }
+}
+
 // A workgroup barrier without a memory fence; the compiler may not move
 // memory operations or MFMAs across it.
 __device__ __forceinline__ void mc_ring_barrier() {
@@ -237,6 +291,35 @@ __device__ __forceinline__ void mc_ring_barrier() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// The store of one unit's accumulators: acc[i][j] value v of lane l is row
+// row0 + 32 i + 8 (v / 4) + v % 4 (row0 includes the lane's 4 (l / 32)),
+// column col + j. The kBJ columns of a lane are stored together: with N a
+// multiple of 4 they are all inside C or all past its edge (the caller skips
+// the latter). kCheck: some rows may be past M. Without it the store is
+// straight-line code, so the compiler can issue the epilogue's operand loads
+// for many rows before the first store instead of one row at a time.
+template <class Cfg, bool kCheck, typename Epilogue>
+__device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ], float* __restrict__ out,
+                                              int row0, int col, int m, int n, bool raw, const Epilogue& epilogue) {
+    typedef McRingVec<Cfg::kBJ> BV;
+#pragma unroll
+    for (int i = 0; i < Cfg::kAI; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+            if (kCheck && row >= m) continue;
+            const long long at = static_cast<long long>(row) * n + col;
+            typename BV::type o;
+#pragma unroll
+            for (int j = 0; j < Cfg::kBJ; ++j) {
+                const float x = acc[i][j][v];
+                BV::set(o, j, raw ? x : epilogue(x, static_cast<unsigned>(at + j)));
+            }
+            *reinterpret_cast<typename BV::type*>(out + at) = o;
+        }
+    }
 }
 
 // The C tiles (and K splits) of an M x N x K product, `splits` splits of
@@ -361,6 +444,17 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
         ws = next(ws);
         advance();
     }
+    // Staged: the registers hold the fetch of step `pre` (loaded, not yet
+    // written). Past the block's last unit the cursor wraps to the start of
+    // that unit, so every load stays in bounds.
+    mc_ring_f32x4 staged[Cfg::kFetch];
+    if constexpr (Cfg::kStaged) {
+        if (total > 0) {
+#pragma unroll
+            for (int idx = 0; idx < Cfg::kFetch; ++idx) staged[idx] = mc_ring_load_one<Cfg>(fetch, ft, idx);
+            advance();
+        }
+    }
 
     int g = 0;  // steps consumed
     for (int ui = 0; ui < count; ++ui) {
@@ -371,15 +465,26 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
 #pragma unroll
             for (int j = 0; j < Cfg::kBJ; ++j) acc[i][j] = mc_ring_f32x16{};
         for (int t = 0; t < u.steps; ++t, ++g) {
-            // Fetch groups issued after the one of step g (stores issued
-            // after it only make the wait longer): wait for that one and for
-            // this wave's LDS reads of the previous step.
-            mc_ring_wait_later<Cfg::kFetch, Cfg::kStages - 2>(issued - g - 1);
+            if constexpr (Cfg::kStaged) {
+                // Step g came from the prologue's direct fetch (g < pre) or
+                // was written to LDS from registers during step g - 1 (and
+                // waited for with the LDS reads below).
+                if (g < pre)
+                    mc_ring_wait_direct<Cfg::kFetch, Cfg::kStages - 2>(pre - 1 - g);
+                else
+                    MC_RING_WAIT(63);
+            } else {
+                // Fetch groups issued after the one of step g (stores issued
+                // after it only make the wait longer): wait for that one and
+                // for this wave's LDS reads of the previous step.
+                mc_ring_wait_later<Cfg::kFetch, Cfg::kStages - 2>(issued - g - 1);
+            }
             // Every wave's fetch of step g has landed, and every wave is done
             // with step g - 1, whose stage the next fetch overwrites.
             mc_ring_barrier();
-            const bool more = issued < total;
-            mc_ring_step<Cfg>(lds + rs * Cfg::kStage, lds + ws * Cfg::kStage, more, fetch, wave, ft, a_off, b_off, acc);
+            const bool more = Cfg::kStaged || issued < total;
+            mc_ring_step<Cfg>(lds + rs * Cfg::kStage, lds + ws * Cfg::kStage, more, fetch, wave, ft, a_off, b_off, acc,
+                              staged);
             rs = next(rs);
             if (more) {
                 ++issued;
@@ -388,28 +493,13 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
             }
         }
 
-        // acc[i][j] value v of lane l: row wr + 32 i + 8 (v / 4) + 4 (l / 32) + v % 4,
-        // column lcol + j. The kBJ columns of a lane are stored together: with
-        // N a multiple of 4 they are all inside C or all past its edge.
         const int col = u.col0 + lcol;
         if (col >= n) continue;
         float* __restrict__ out = splits > 1 ? partial + static_cast<long long>(u.split) * m * n : c;
-#pragma unroll
-        for (int i = 0; i < Cfg::kAI; ++i) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = u.row0 + wr + 32 * i + 8 * (v >> 2) + 4 * half + (v & 3);
-                if (row >= m) continue;
-                const long long at = static_cast<long long>(row) * n + col;
-                typename BV::type o;
-#pragma unroll
-                for (int j = 0; j < Cfg::kBJ; ++j) {
-                    const float x = acc[i][j][v];
-                    BV::set(o, j, splits > 1 ? x : epilogue(x, static_cast<unsigned>(at + j)));
-                }
-                *reinterpret_cast<typename BV::type*>(out + at) = o;
-            }
-        }
+        if (u.row0 + Cfg::kBM <= m)
+            mc_ring_store<Cfg, false>(acc, out, u.row0 + wr + 4 * half, col, m, n, splits > 1, epilogue);
+        else
+            mc_ring_store<Cfg, true>(acc, out, u.row0 + wr + 4 * half, col, m, n, splits > 1, epilogue);
     }
     MC_RING_WAIT(0);
 }

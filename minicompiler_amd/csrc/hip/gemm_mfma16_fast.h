@@ -157,6 +157,32 @@ __device__ __forceinline__ void step_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// The store of a wave's accumulators: acc[fi][fj] holds
+// C[row + 16 fi][col + 16 fj + v] (row, col include the lane's l % 16 and
+// 4 (l / 16)). kCheck: some rows or columns may be past the matrix edge.
+// Without it the store is straight-line code, so the compiler can issue the
+// epilogue's operand loads for many fragments before the first store.
+template <bool kCheck, typename Epilogue>
+__device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kFRowFrags][kFColFrags], float* __restrict__ c,
+                                           int row, int col, int m, int n, const Epilogue& epilogue) {
+#pragma unroll
+    for (int fi = 0; fi < kFRowFrags; ++fi) {
+        const int r = row + fi * 16;
+        if (kCheck && r >= m) continue;
+        float* crow = c + static_cast<long long>(r) * n;
+#pragma unroll
+        for (int fj = 0; fj < kFColFrags; ++fj) {
+            const int cc = col + fj * 16;
+            if (kCheck && cc >= n) continue;
+            const unsigned at = static_cast<unsigned>(static_cast<long long>(r) * n + cc);
+            mc_f32x4_t v = acc[fi][fj];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = epilogue(v[e], at + e);
+            *reinterpret_cast<mc_f32x4_t*>(crow + cc) = v;
+        }
+    }
+}
+
 // The block's 256x256 tile of C (grid: one block per tile, row-major); the
 // epilogue maps each accumulated value v of element i = row n + col to what
 // is stored.
@@ -249,22 +275,8 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
     if (!late) step_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
-    // acc[fi][fj] holds C[row0 + wr + 16 fi + l % 16][col0 + wc + 16 fj + 4 (l / 16) + v].
-#pragma unroll
-    for (int fi = 0; fi < kFRowFrags; ++fi) {
-        const int row = row0 + wr + fi * 16 + li;
-        if (row >= m) continue;
-        float* crow = c + static_cast<long long>(row) * n;
-#pragma unroll
-        for (int fj = 0; fj < kFColFrags; ++fj) {
-            const int col = col0 + wc + fj * 16 + 4 * g;
-            if (col >= n) continue;
-            const unsigned at = static_cast<unsigned>(static_cast<long long>(row) * n + col);
-            mc_f32x4_t v = acc[fi][fj];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = epilogue(v[e], at + e);
-            *reinterpret_cast<mc_f32x4_t*>(crow + col) = v;
-        }
-    }
+    if (row0 + kFBM <= m && col0 + kFBN <= n)
+        fast_store<false>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+    else
+        fast_store<true>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
 }
-

@@ -508,7 +508,6 @@ private:
             case MCHIP_RING_BIG: return GemmBody::F32RingBig;
             case MCHIP_RING_THIN: return GemmBody::F32RingThin;
             case MCHIP_RING_WIDE: return GemmBody::F32RingWide;
-            case MCHIP_RING_DEEP: return GemmBody::F32RingDeep;
             default: return GemmBody::F32Mfma;
         }
     }

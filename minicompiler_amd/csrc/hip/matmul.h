@@ -42,14 +42,13 @@ int mchip_matmul_blocks_per_cu(int kernel);
  *   MCHIP_RING_NONE  the shape does not fit it (K not a multiple of 32, or N
  *                    not a multiple of 4): the two-stage body runs instead;
  *   MCHIP_RING_BIG   one persistent block of 4 waves per CU, 256x256 tiles;
- *   MCHIP_RING_WIDE  two persistent blocks of 4 waves per CU, 128x128 tiles;
- *   MCHIP_RING_DEEP  one persistent block of 4 waves per CU, 128x128 tiles,
- *                    4 LDS stages;
+ *   MCHIP_RING_WIDE  up to two persistent blocks of 4 waves per CU, 128x128
+ *                    tiles, the fetch staged through registers;
  *   MCHIP_RING_THIN  for m <= 32: 32x128 tiles, 6 LDS stages.
  * The choice minimises (rounds of tiles per CU) x (work per tile) / (the
  * configuration's measured efficiency). *grid receives the number of
  * blocks, *block the lanes per block. */
-enum { MCHIP_RING_NONE = 0, MCHIP_RING_WIDE = 1, MCHIP_RING_DEEP = 2, MCHIP_RING_BIG = 3, MCHIP_RING_THIN = 4 };
+enum { MCHIP_RING_NONE = 0, MCHIP_RING_WIDE = 1, MCHIP_RING_BIG = 3, MCHIP_RING_THIN = 4 };
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 
 /* Elementwise fp32 -> bf16/fp16 (round to nearest even), for staging. */

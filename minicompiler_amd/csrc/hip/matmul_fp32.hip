@@ -157,7 +157,6 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
 
 using RingBig = McRingBig;
 using RingWide = McRingWide;
-using RingDeep = McRingDeep;
 using RingThin = McRingThin;
 constexpr int kRBKRing = RingWide::kBK;
 
@@ -234,9 +233,6 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     } else if (ring == MCHIP_RING_WIDE) {
         hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws);
-    } else if (ring == MCHIP_RING_DEEP) {
-        hipLaunchKernelGGL((matmul_ring_f32<RingDeep, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
-                           k, k_split, depth, out_ws);
     } else if (double_buffer) {
         if (vec) {
             hipLaunchKernelGGL((matmul_mfma_f32<true, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
@@ -263,11 +259,11 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     if (m < 1 || n < 4 || k < kRBKRing || k % kRBKRing != 0 || n % 4 != 0 || depth < 1 || cu_count < 1) {
         return MCHIP_RING_NONE;
     }
-    // Time in units of one 128x128 tile-split on a whole CU: rounds of
-    // tile-splits per block slot x work per tile-split (a 256x256 tile is
-    // four; two blocks sharing a CU each run at half speed) / efficiency
-    // (measured on 8192^3, 4096^3 and the MLP shapes: about 0.92, 0.86 and
-    // 0.80 of the matrix peak inside the main loop).
+    // Time in units of one 128x128 tile-split on a whole CU: the tile-splits
+    // of the busiest CU x work per tile-split (a 256x256 tile is four) /
+    // efficiency (big and wide measured within 1% of each other on 8192^3,
+    // 4096^3 and the MLP's first GEMM, where both fill every CU; wide with
+    // one block per CU as efficient per tile as with two).
     const long long cus = cu_count;
     if (m <= RingThin::kBM) {
         const long long t32 = static_cast<long long>((n + 127) / 128) * depth;
@@ -278,21 +274,16 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     const long long t256 = static_cast<long long>((m + 255) / 256) * ((n + 255) / 256) * depth;
     const long long t128 = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
     const double big = static_cast<double>((t256 + cus - 1) / cus) * 4.0 / 0.92;
-    const double wide = static_cast<double>((t128 + 2 * cus - 1) / (2 * cus)) * 2.0 / 0.86;
-    const double deep = static_cast<double>((t128 + cus - 1) / cus) * 1.0 / 0.80;
-    if (big <= wide && big <= deep) {
+    const long long wide_grid = std::min(t128, 2 * cus);
+    const double wide = static_cast<double>((wide_grid > cus ? 2 : 1) * ((t128 + wide_grid - 1) / wide_grid)) / 0.91;
+    if (big <= wide) {
         *grid = static_cast<unsigned>(std::min(t256, cus));
         *block = RingBig::kThreads;
         return MCHIP_RING_BIG;
     }
-    if (wide <= deep) {
-        *grid = static_cast<unsigned>(std::min(t128, 2 * cus));
-        *block = RingWide::kThreads;
-        return MCHIP_RING_WIDE;
-    }
-    *grid = static_cast<unsigned>(std::min(t128, cus));
-    *block = RingDeep::kThreads;
-    return MCHIP_RING_DEEP;
+    *grid = static_cast<unsigned>(wide_grid);
+    *block = RingWide::kThreads;
+    return MCHIP_RING_WIDE;
 }
 
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {

@@ -92,6 +92,12 @@ struct HipOptions {
     // legacy null stream). enqueue_launch and enqueue_with_events launch
     // directly.
     bool graph_replay = false;
+    // An Auto FP32 matmul's K split is chosen by timing the candidates on the
+    // device at compile time (double_buffered unsplit or split_k with 2, 4, ...
+    // splits) instead of by the split rule. Decisions are kept per device and
+    // shape for the process, and in MINICOMPILER_HIP_CACHE_DIR when set.
+    // Different split counts round differently (within the FP32 GEMM bound).
+    bool autotune = false;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).

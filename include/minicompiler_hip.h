@@ -70,9 +70,12 @@ MC_API void mc_release(void* handle); /* capi.cpp:233-235 */
 /* ---- Part 2: extensions ---------------------------------------------------- */
 
 /* mc_compile from graph text, with backend options
- * "matmul=NAME,vectorize=0|1,device=N,epilogue=0|1,tc_convert=0|1,graph=0|1"
- * (graph=1: mc_enqueue captures its launches into a HIP graph once and
- * replays it; rebinding buffers captures again) and the elementwise
+ * "matmul=NAME,vectorize=0|1,device=N,epilogue=0|1,tc_convert=0|1,graph=0|1,
+ * autotune=0|1" (graph=1: mc_enqueue captures its launches into a HIP graph
+ * once and replays it; rebinding buffers captures again. autotune=1: an
+ * auto FP32 matmul's K split is chosen by timing the candidates on the
+ * device at compile time, kept per shape for the process and in
+ * MINICOMPILER_HIP_CACHE_DIR when set) and the elementwise
  * kernel shape "ew_items=N,ew_nt_loads=0|1,ew_nt_stores=0|1,
  * ew_blocks_per_cu=N" (NULL or "" for defaults). */
 MC_API void* mc_compile_source(const char* text, const char* dims, const char* passes, const char* backend,

@@ -124,14 +124,16 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             o.fuse_epilogue = value != "0" && value != "false";
         } else if (key == "graph") {
             o.graph_replay = value != "0" && value != "false";
+        } else if (key == "autotune") {
+            o.autotune = value != "0" && value != "false";
         } else if (key == "ew_nt_loads") {
             o.nontemporal_loads = value != "0" && value != "false";
         } else if (key == "ew_nt_stores") {
             o.nontemporal_stores = value != "0" && value != "false";
         } else {
             return Error{"unknown option '" + key +
-                         "' (matmul, vectorize, device, epilogue, graph, tc_convert, ew_items, ew_nt_loads, "
-                         "ew_nt_stores, ew_blocks_per_cu)"};
+                         "' (matmul, vectorize, device, epilogue, graph, autotune, tc_convert, ew_items, "
+                         "ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
         }
     }
     return o;

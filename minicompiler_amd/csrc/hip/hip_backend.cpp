@@ -12,6 +12,7 @@
 
 #include "minicompiler/hip/hip_backend.hpp"
 
+#include "autotune.hpp"
 #include "codegen.hpp"
 #include "hip_rt.h"
 #include "kernel_compiler.hpp"
@@ -485,6 +486,14 @@ private:
                          "): gfx950 has bf16 and fp16 matrix instructions but no xf32 (TF32) one"};
         }
         l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
+        if (options_.autotune && options_.matmul == MatmulKernel::Auto) {
+            // The split count timed on this device (double_buffered unsplit,
+            // split_k otherwise) instead of the split rule's.
+            Result<int> tuned = autotune_fp32_splits(device_, l->m, l->n, l->k);
+            if (!tuned.ok()) return tuned.error();
+            l->splits = tuned.value();
+            l->matmul = l->splits > 1 ? MatmulKernel::SplitK : MatmulKernel::DoubleBuffered;
+        }
         const bool bf16 = l->matmul == MatmulKernel::TensorCoreBf16, f16 = l->matmul == MatmulKernel::TensorCoreF16;
         if (options_.convert_tensor_core_operands && (bf16 || f16) && l->k % 64 == 0 && l->n % 8 == 0 && l->n >= 8) {
             l->lowp = true;

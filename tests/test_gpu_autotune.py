@@ -1,0 +1,83 @@
+"""Compile-time autotuning of the FP32 matmul's K split (option autotune=1):
+the MLP at B=256 and B=1024 (each GEMM has fewer 128x128 tiles than two
+per CU, so several split counts are timed) matches the CPU oracle within
+the FP32 tolerance, the decisions land in MINICOMPILER_HIP_CACHE_DIR, and a
+second process reads them instead of timing and computes the same bits.
+(The reference fixes the split by a rule, src/cuda/matmul_kernels.cu:352-367;
+tuning it on the device is this build's.)"""
+
+import json
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, max_abs
+
+pytestmark = pytest.mark.gpu
+
+REPO = Path(__file__).resolve().parents[1]
+SCRIPT = """
+import json, sys, time
+import numpy as np
+sys.path.insert(0, {repo!r})
+import minicompiler_amd as mc
+from oracle import oracle
+out = {{}}
+for b in (256, 1024):
+    t0 = time.perf_counter()
+    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={{"B": b}}, options={{"autotune": 1}})
+    compile_s = time.perf_counter() - t0
+    x = oracle.uniform(c.input_sizes[0], 7, -1.0, 1.0)
+    y = c.run([x])[0]
+    np.save({out!r} + f"/y{{b}}.npy", y)
+    out[b] = {{"kernels": list(c.matmul_kernels), "compile_s": compile_s,
+               "bits": int(np.bitwise_xor.reduce(y.view(np.uint32)))}}
+print(json.dumps(out))
+"""
+
+
+def run_child(cache_dir: Path, out_dir: Path) -> dict:
+    env = {**os.environ, "MINICOMPILER_HIP_CACHE_DIR": str(cache_dir)}
+    print(f"case autotune child {cache_dir}", flush=True)
+    r = subprocess.run([sys.executable, "-c", SCRIPT.format(repo=str(REPO), out=str(out_dir))], env=env,
+                       capture_output=True, text=True, timeout=150)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return {int(k): v for k, v in json.loads(r.stdout.strip().splitlines()[-1]).items()}
+
+
+def decision_lines(cache_dir: Path) -> list[str]:
+    files = sorted(cache_dir.glob("autotune_*.txt"))
+    assert len(files) == 1, files
+    return files[0].read_text().splitlines()
+
+
+def test_autotuned_splits_stay_within_the_fp32_bound_and_are_reused(device, mc, oracle, tmp_path):
+    cache, out1, out2 = tmp_path / "cache", tmp_path / "o1", tmp_path / "o2"
+    for d in (cache, out1, out2):
+        d.mkdir()
+    first = run_child(cache, out1)
+    lines = decision_lines(cache)
+    shapes = {tuple(int(v) for v in line.split()[:3]) for line in lines}
+    # (m, n, k) of GEMM1 (B x 2048 x 512) and GEMM2 (B x 512 x 2048).
+    assert shapes == {(256, 2048, 512), (256, 512, 2048), (1024, 2048, 512), (1024, 512, 2048)}, lines
+    for line in lines:
+        m, n, k, s = (int(v) for v in line.split())
+        assert s in (1, 2, 4, 8, 16, 32, 64) and s <= max(1, k // 64), line
+    for b in (256, 1024):
+        assert set(first[b]["kernels"]) <= {"double_buffered", "split_k"}
+        c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": b}, backend="none")
+        x = oracle.uniform(c.input_sizes[0], 7, -1.0, 1.0)
+        cpu = oracle.evaluate_compiled(c, [x])[0]
+        y = np.load(out1 / f"y{b}.npy")
+        assert_close(y, cpu, 1e-4, 1e-4 * max(1.0, max_abs(cpu)), f"autotuned mlp B={b}")
+    # A second process finds every decision on disk: no new lines, same
+    # kernels, same bits.
+    second = run_child(cache, out2)
+    assert decision_lines(cache) == lines
+    for b in (256, 1024):
+        assert second[b]["kernels"] == first[b]["kernels"]
+        assert second[b]["bits"] == first[b]["bits"]

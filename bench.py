@@ -265,9 +265,10 @@ def bench_gemm_lowp(mc, shapes, steps: int, warmup: int) -> list[dict]:
 def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
     """BASELINE config 5 with its epilogue: matmul_bias_gelu.mcg (y =
     gelu_tanh(x w + bias), fp32 in and out) compiled with the bf16 / fp16
-    matrix-core kernel. A step rounds x to 16 bits (w once, at compile time)
-    and runs the GEMM with bias+GELU fused into its store; the GEMM launch is
-    also timed alone."""
+    matrix-core kernel. A step is one launch: it rounds x to 16 bits (w was
+    rounded once, at compile time), then runs the GEMM with bias+GELU fused
+    into its store; `gemm_epilogue_tflops` counts the GEMM's 2MNK FLOPs over
+    that whole launch, the rounding of x included (about 0.1 ms at 8192^2)."""
     out = []
     for m, n, k in shapes:
         for kernel in ("tensor_core_bf16", "tensor_core_f16"):

@@ -89,28 +89,40 @@ constexpr int kFWaves = kFThreads / 64;
 constexpr int kFStages = 4;
 constexpr int kFStage = 32 * 1024;
 constexpr int kFBOffset = 16 * 1024;
-constexpr int kFRowFrags = 8;  // 16-row A fragments per wave (128 rows)
 constexpr int kFColFrags = 4;  // 16-column B fragments per wave (64 columns)
-// global_load_lds instructions per wave per step: 2 for A, 2 for B.
-constexpr int kFFetchPerStep = 4;
 
 __device__ __forceinline__ int swz_b(int kr) { return (kr & 3) | (((kr >> 3) & 3) << 2); }
 
+// A block tile of kRows x 256 (kRows = 256, or 128 for the halves of the
+// last tiles): wave (wm, wn) of the 2x4 grid owns kRows / 2 rows as
+// kRows / 32 A fragments of 16 rows. A stage holds kRows A rows (kRows / 128
+// global_load_lds instructions per wave and step) and 32 k rows of B (2 per
+// wave).
+template <int kRows>
+struct FastShape {
+    static constexpr int kRowFrags = kRows / 32;
+    static constexpr int kFetchA = kRows / 128;
+    static constexpr int kFetch = kFetchA + 2;
+};
+
 // Per-lane addressing, set up once per block.
+template <int kRows>
 struct FastLane {
-    const unsigned short* a_src[2];  // A chunk this lane fetches per instruction (k offset 0)
-    const unsigned short* b_src[2];  // B chunk (k row offset 0)
-    long long b_step;           // elements between consecutive K steps of B
-    int a_off[kFRowFrags];           // LDS byte offsets of the A fragments
-    int b_off[2][kFColFrags];        // LDS byte offsets of the two transposed B reads
+    const unsigned short* a_src[FastShape<kRows>::kFetchA];  // A chunk this lane fetches per instruction (k offset 0)
+    const unsigned short* b_src[2];                          // B chunk (k row offset 0)
+    long long b_step;                                        // elements between consecutive K steps of B
+    int a_off[FastShape<kRows>::kRowFrags];                  // LDS byte offsets of the A fragments
+    int b_off[2][kFColFrags];                                // LDS byte offsets of the two transposed B reads
     int wave;
 };
 
-__device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastLane& L, int fetch_k) {
-    MC_LDS unsigned char* sa = wr + L.wave * 32 * 64;
+template <int kRows>
+__device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastLane<kRows>& L, int fetch_k) {
+    constexpr int kFA = FastShape<kRows>::kFetchA;
+    MC_LDS unsigned char* sa = wr + L.wave * kFA * 1024;
     MC_LDS unsigned char* sb = wr + kFBOffset + L.wave * 4 * 512;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kFA; ++i) {
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.a_src[i] + fetch_k),
                                          reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
     }
@@ -122,11 +134,13 @@ __device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastL
     }
 }
 
-__device__ __forceinline__ mc_u16x8_t fast_read_a(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
+template <int kRows>
+__device__ __forceinline__ mc_u16x8_t fast_read_a(const MC_LDS unsigned char* rd, const FastLane<kRows>& L, int f) {
     return *reinterpret_cast<const MC_LDS mc_u16x8_t*>(rd + L.a_off[f]);
 }
 
-__device__ __forceinline__ mc_u16x8_t fast_read_b(const MC_LDS unsigned char* rd, const FastLane& L, int f) {
+template <int kRows>
+__device__ __forceinline__ mc_u16x8_t fast_read_b(const MC_LDS unsigned char* rd, const FastLane<kRows>& L, int f) {
     MC_LDS unsigned char* p = const_cast<MC_LDS unsigned char*>(rd);
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[0][f]));
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<MC_LDS s16x4*>(p + L.b_off[1][f]));
@@ -137,14 +151,16 @@ __device__ __forceinline__ mc_u16x8_t fast_read_b(const MC_LDS unsigned char* rd
 // step held in `rd` into (av, bv). `rd` and `wr` are distinct stages;
 // declaring them __restrict__ gives the LDS reads alias scopes that keep the
 // compiler from making them wait for the fetch.
+template <int kRows>
 __device__ __forceinline__ void fast_memory_phase(const MC_LDS unsigned char* __restrict__ rd,
-                                                  MC_LDS unsigned char* __restrict__ wr, const FastLane& L, int fetch_k,
-                                                  mc_u16x8_t (&av)[kFRowFrags], mc_u16x8_t (&bv)[kFColFrags]) {
-    fast_fetch(wr, L, fetch_k);
+                                                  MC_LDS unsigned char* __restrict__ wr, const FastLane<kRows>& L,
+                                                  int fetch_k, mc_u16x8_t (&av)[FastShape<kRows>::kRowFrags],
+                                                  mc_u16x8_t (&bv)[kFColFrags]) {
+    fast_fetch<kRows>(wr, L, fetch_k);
 #pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) av[f] = fast_read_a(rd, L, f);
+    for (int f = 0; f < FastShape<kRows>::kRowFrags; ++f) av[f] = fast_read_a<kRows>(rd, L, f);
 #pragma unroll
-    for (int f = 0; f < kFColFrags; ++f) bv[f] = fast_read_b(rd, L, f);
+    for (int f = 0; f < kFColFrags; ++f) bv[f] = fast_read_b<kRows>(rd, L, f);
 }
 
 // A workgroup barrier without a memory fence; the compiler may not move
@@ -162,11 +178,11 @@ __device__ __forceinline__ void step_barrier() {
 // 4 (l / 16)). kCheck: some rows or columns may be past the matrix edge.
 // Without it the store is straight-line code, so the compiler can issue the
 // epilogue's operand loads for many fragments before the first store.
-template <bool kCheck, typename Epilogue>
-__device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kFRowFrags][kFColFrags], float* __restrict__ c,
+template <int kRowFrags, bool kCheck, typename Epilogue>
+__device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kRowFrags][kFColFrags], float* __restrict__ c,
                                            int row, int col, int m, int n, const Epilogue& epilogue) {
 #pragma unroll
-    for (int fi = 0; fi < kFRowFrags; ++fi) {
+    for (int fi = 0; fi < kRowFrags; ++fi) {
         const int r = row + fi * 16;
         if (kCheck && r >= m) continue;
         float* crow = c + static_cast<long long>(r) * n;
@@ -183,30 +199,22 @@ __device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kFRowFrags][k
     }
 }
 
-// The block's 256x256 tile of C (grid: one block per tile, row-major); the
-// epilogue maps each accumulated value v of element i = row n + col to what
-// is stored.
-template <bool kBf16, typename Epilogue>
-__device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b,
-                                               float* __restrict__ c, int m, int n, int k, const Epilogue& epilogue) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[kFStages * kFStage];
-    MC_LDS unsigned char* lds = (MC_LDS unsigned char*)(smem);  // generic -> LDS address space
-
+// One kRows x 256 tile of C at (row0, col0), all of K.
+template <bool kBf16, int kRows, typename Epilogue>
+__device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsigned short* __restrict__ a,
+                                          const unsigned short* __restrict__ b, float* __restrict__ c, int m, int n,
+                                          int k, int row0, int col0, const Epilogue& epilogue) {
+    typedef FastShape<kRows> Sh;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
 
-    // Tile of this block (row-major).
-    const int tiles_n = (n + kFBN - 1) / kFBN;
-    const int tm = static_cast<int>(blockIdx.x) / tiles_n, tn = static_cast<int>(blockIdx.x) % tiles_n;
-    const int row0 = tm * kFBM, col0 = tn * kFBN;
-
-    FastLane L;
+    FastLane<kRows> L;
     L.wave = wave;
-    // A: wave w fills the 16-row blocks 2 w and 2 w + 1, one per
-    // instruction; lane -> (row 32 w + 16 i + l % 16, chunk l / 16).
+    // A: wave w fills the 16-row blocks kFetchA w + i, one per instruction;
+    // lane -> (row 16 (kFetchA w + i) + l % 16, chunk l / 16).
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = wave * 32 + i * 16 + (lane & 15);
+    for (int i = 0; i < Sh::kFetchA; ++i) {
+        const int r = (wave * Sh::kFetchA + i) * 16 + (lane & 15);
         const int gr = mc_min16(row0 + r, m - 1);
         L.a_src[i] = a + static_cast<long long>(gr) * k + (lane >> 4) * 8;
     }
@@ -220,11 +228,11 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
         L.b_src[i] = b + static_cast<long long>(kr) * n + gc;
     }
     L.b_step = static_cast<long long>(kFBK) * n;
-    // Wave (wm, wn) of the 2x4 grid owns rows 128 wm .., columns 64 wn ...
-    const int wr = (wave >> 2) * 128, wc = (wave & 3) * 64;
+    // Wave (wm, wn) of the 2x4 grid owns rows kRows / 2 wm .., columns 64 wn ...
+    const int wr = (wave >> 2) * (kRows / 2), wc = (wave & 3) * 64;
     const int li = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int f = 0; f < kFRowFrags; ++f) L.a_off[f] = (wr + f * 16) * 64 + lane * 16;
+    for (int f = 0; f < Sh::kRowFrags; ++f) L.a_off[f] = (wr + f * 16) * 64 + lane * 16;
     // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
     // k row 8 g + 4 h + e, columns n0 + 4 cc .. + 3.
     const int te = (lane & 15) >> 2, tc = lane & 3;
@@ -238,18 +246,18 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
             L.b_off[h][f] = kFBOffset + kr * 512 + (chunk << 4) + ((ncol & 4) << 1);
         }
 
-    mc_f32x4_t acc[kFRowFrags][kFColFrags];
+    mc_f32x4_t acc[Sh::kRowFrags][kFColFrags];
 #pragma unroll
-    for (int i = 0; i < kFRowFrags; ++i)
+    for (int i = 0; i < Sh::kRowFrags; ++i)
 #pragma unroll
         for (int j = 0; j < kFColFrags; ++j) acc[i][j] = mc_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int steps = k / kFBK;
     auto stage = [&](int t) { return lds + (t & (kFStages - 1)) * kFStage; };
-    mc_u16x8_t av[kFRowFrags], bv[kFColFrags];
+    mc_u16x8_t av[Sh::kRowFrags], bv[kFColFrags];
     // Prologue: steps 0..2 landed.
     const int pre = mc_min16(steps, kFStages - 1);
-    for (int t = 0; t < pre; ++t) fast_fetch(stage(t), L, t * kFBK);
+    for (int t = 0; t < pre; ++t) fast_fetch<kRows>(stage(t), L, t * kFBK);
     __builtin_amdgcn_s_waitcnt(0);
     step_barrier();
     // Waves 4-7 start one phase late.
@@ -263,11 +271,11 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
     // phases later.
     const int last = (steps - 1) * kFBK;
     for (int t = 0; t < steps; ++t) {
-        fast_memory_phase(stage(t), stage(t + 3), L, mc_min16((t + 3) * kFBK, last), av, bv);
-        __builtin_amdgcn_s_waitcnt(0x0070 | (2 * kFFetchPerStep));  // vmcnt(8), lgkmcnt(0)
+        fast_memory_phase<kRows>(stage(t), stage(t + 3), L, mc_min16((t + 3) * kFBK, last), av, bv);
+        __builtin_amdgcn_s_waitcnt(0x0070 | (2 * Sh::kFetch));  // vmcnt(2 kFetch), lgkmcnt(0)
         step_barrier();
 #pragma unroll
-        for (int fi = 0; fi < kFRowFrags; ++fi)
+        for (int fi = 0; fi < Sh::kRowFrags; ++fi)
 #pragma unroll
             for (int fj = 0; fj < kFColFrags; ++fj) acc[fi][fj] = mc_mfma16<kBf16>(bv[fj], av[fi], acc[fi][fj]);
         step_barrier();
@@ -275,8 +283,38 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
     if (!late) step_barrier();
     __builtin_amdgcn_s_waitcnt(0);
 
-    if (row0 + kFBM <= m && col0 + kFBN <= n)
-        fast_store<false>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+    if (row0 + kRows <= m && col0 + kFBN <= n)
+        fast_store<Sh::kRowFrags, false>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
     else
-        fast_store<true>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+        fast_store<Sh::kRowFrags, true>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+}
+
+// C = A B with the epilogue mapping each accumulated value v of element
+// i = row n + col to what is stored. The tiles are 256x256 in row-major
+// order; the grid has one block per tile plus `halves` = gridDim.x - tiles
+// more: the last `halves` tiles each run as two blocks of 128 x 256 (rows
+// 0-127 and 128-255), so a last round that would fill at most half of the
+// CUs (896 tiles on 256 CUs: 3 rounds and 128 tiles) runs at half the work
+// per block on all of them (mchip_mfma16_fast_grid picks the count). Every C
+// element gets the same MFMA sequence either way, so the results are the
+// same bits.
+template <bool kBf16, typename Epilogue>
+__device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b,
+                                               float* __restrict__ c, int m, int n, int k, const Epilogue& epilogue) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kFStages * kFStage];
+    MC_LDS unsigned char* lds = (MC_LDS unsigned char*)(smem);  // generic -> LDS address space
+
+    const int tiles_n = (n + kFBN - 1) / kFBN;
+    const int tiles = ((m + kFBM - 1) / kFBM) * tiles_n;
+    const int halves = static_cast<int>(gridDim.x) - tiles;
+    const int full = tiles - halves;
+    const int bid = static_cast<int>(blockIdx.x);
+    if (bid < full) {
+        const int tm = bid / tiles_n, tn = bid % tiles_n;
+        fast_tile<kBf16, kFBM>(lds, a, b, c, m, n, k, tm * kFBM, tn * kFBN, epilogue);
+    } else {
+        const int t = full + (bid - full) / 2, half = (bid - full) % 2;
+        const int tm = t / tiles_n, tn = t % tiles_n;
+        fast_tile<kBf16, kFBM / 2>(lds, a, b, c, m, n, k, tm * kFBM + half * (kFBM / 2), tn * kFBN, epilogue);
+    }
 }

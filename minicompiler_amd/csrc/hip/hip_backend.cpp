@@ -638,7 +638,7 @@ private:
             sources_.push_back(kern.source);
             if (l.kind == Launch::Kind::FusedMatmul && l.lowp) {
                 l.function = built[j]->function;
-                l.grid_x = static_cast<unsigned>(((l.m + 255) / 256) * ((l.n + 255) / 256));
+                l.grid_x = mchip_mfma16_fast_grid(l.m, l.n, device_.cu_count);
                 l.grid_y = l.grid_z = 1;
                 l.epilogue_inputs.assign(graph_.node(l.epilogue_node).inputs.size(), nullptr);
                 continue;

@@ -30,6 +30,12 @@ int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b
 /* C = sum over z of partial[z * count + i], added in z order. */
 int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
 
+/* Blocks of the bf16/fp16 256x256-tile kernel (gemm_mfma16_fast.h) for an
+ * m x n product on `cu_count` CUs: one per tile, plus one more for each of
+ * the last tiles when they would fill at most half of the CUs in their round
+ * (those tiles then run as two 128-row halves). */
+unsigned mchip_mfma16_fast_grid(int m, int n, int cu_count);
+
 /* Whether gfx950 runs `kernel` (all but TensorCoreTf32). */
 int mchip_matmul_supported(int kernel);
 

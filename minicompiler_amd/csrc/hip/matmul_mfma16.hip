@@ -22,6 +22,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "gemm_mfma16_fast.h"
 
 #include <algorithm>
@@ -220,13 +222,28 @@ bool fast_eligible(const void* a, const void* b, const float* c, int m, int n, i
     return splits <= 1 && k % (2 * kFBK) == 0 && n % 8 == 0 && al(a) && al(b) && al(c) && m >= 1 && n >= 8;
 }
 
+// CUs of the current device, asked once per device.
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev >= 0 && dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
 template <bool kBf16>
 int launch_fast(const void* a, const void* b, float* c, int m, int n, int k, hipStream_t stream) {
     const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
-    if (tiles > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(static_cast<unsigned>(tiles)), dim3(kFThreads), 0,
-                       stream, static_cast<const unsigned short*>(a), static_cast<const unsigned short*>(b), c, m, n,
-                       k);
+    if (tiles > 0x3fffffffLL) return hipErrorInvalidValue;
+    const unsigned grid = mchip_mfma16_fast_grid(m, n, device_cus());
+    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(grid), dim3(kFThreads), 0, stream,
+                       static_cast<const unsigned short*>(a), static_cast<const unsigned short*>(b), c, m, n, k);
     return hipGetLastError();
 }
 
@@ -293,6 +310,13 @@ extern "C" int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, co
         return fast ? launch_fast<false>(a, b, c, m, n, k, s) : launch16<false, false>(a, b, c, m, n, k, s, splits, workspace);
     }
     return hipErrorInvalidValue;
+}
+
+extern "C" unsigned mchip_mfma16_fast_grid(int m, int n, int cu_count) {
+    const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
+    const long long rest = cu_count > 0 ? tiles % cu_count : 0;
+    const long long halves = rest != 0 && 2 * rest <= cu_count ? rest : 0;
+    return static_cast<unsigned>(tiles + halves);
 }
 
 extern "C" int mchip_matmul_supported(int kernel) { return kernel != kTensorCoreTf32; }

@@ -71,7 +71,10 @@ def test_pre_cast_gemm_at_8192_cubed_on_sampled_elements(device, mc, oracle, ker
     assert np.max(np.abs(got - exact)) <= np.sqrt(k) * (2.0 ** -8 if dtype == 1 else 2.0 ** -11)
 
 
-GRAPH_SHAPES = [(300, 256, 520), (256, 512, 256), (64, 64, 8)]
+# On 256 CUs: 6 and 1 tiles of 256x256 (each run as two 128-row halves),
+# then 272 tiles with M ragged (256 whole tiles and the last 16 as halves,
+# the second half of each partly past M).
+GRAPH_SHAPES = [(300, 256, 520), (256, 512, 256), (64, 64, 8), (4300, 64, 4096)]
 
 
 @pytest.mark.parametrize("kernel", ["tensor_core_bf16", "tensor_core_f16"])

@@ -283,6 +283,41 @@ __global__ void __launch_bounds__(256) convert_kernel(const float* __restrict__ 
     }
 }
 
+// The same rounding on 16-byte-aligned `in` and 8-byte-aligned `out`: a lane
+// reads a float4 and writes its four 16-bit values as one 8-byte store, for
+// kConvertItems float4s spaced one block apart (each wave instruction reads
+// 1 KiB and writes 512 bytes of consecutive memory). Elements past the last
+// whole float4 are done one by one by the first block.
+constexpr int kConvertItems = 4;
+
+template <bool kBf16>
+__global__ void __launch_bounds__(256) convert_vec_kernel(const f32x4* __restrict__ in, u16x4* __restrict__ out,
+                                                          std::size_t groups, const float* __restrict__ tail_in,
+                                                          unsigned short* __restrict__ tail_out, int tail) {
+    const std::size_t span = static_cast<std::size_t>(256) * kConvertItems;
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * span;
+    for (std::size_t base = static_cast<std::size_t>(blockIdx.x) * span + threadIdx.x; base < groups; base += stride) {
+        f32x4 v[kConvertItems];
+#pragma unroll
+        for (int j = 0; j < kConvertItems; ++j) {
+            const std::size_t g = base + static_cast<std::size_t>(j) * 256;
+            if (g < groups) v[j] = __builtin_nontemporal_load(in + g);
+        }
+#pragma unroll
+        for (int j = 0; j < kConvertItems; ++j) {
+            const std::size_t g = base + static_cast<std::size_t>(j) * 256;
+            if (g < groups) {
+                const u16x4 r = {to_bits<kBf16>(v[j][0]), to_bits<kBf16>(v[j][1]), to_bits<kBf16>(v[j][2]),
+                                 to_bits<kBf16>(v[j][3])};
+                out[g] = r;
+            }
+        }
+    }
+    if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < tail) {
+        tail_out[threadIdx.x] = to_bits<kBf16>(tail_in[threadIdx.x]);
+    }
+}
+
 }  // namespace
 
 extern "C" int mchip_launch_tensor_core(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
@@ -342,8 +377,29 @@ extern "C" int mchip_matmul_blocks_per_cu(int kernel) {
 
 extern "C" int mchip_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream) {
     if (dtype != MCHIP_DTYPE_BF16 && dtype != MCHIP_DTYPE_F16) return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (count == 0) return hipSuccess;
+    if (reinterpret_cast<std::uintptr_t>(in) % 16 == 0 && reinterpret_cast<std::uintptr_t>(out) % 8 == 0) {
+        const std::size_t groups = count / 4;
+        const int tail = static_cast<int>(count % 4);
+        const std::size_t per_block = static_cast<std::size_t>(256) * kConvertItems;
+        const unsigned blocks =
+            static_cast<unsigned>(std::max<std::size_t>(1, std::min<std::size_t>((groups + per_block - 1) / per_block, 8192)));
+        const float* tail_in = in + groups * 4;
+        unsigned short* tail_out = static_cast<unsigned short*>(out) + groups * 4;
+        if (dtype == MCHIP_DTYPE_BF16) {
+            hipLaunchKernelGGL(convert_vec_kernel<true>, dim3(blocks), dim3(256), 0, s,
+                               reinterpret_cast<const f32x4*>(in), static_cast<u16x4*>(out), groups, tail_in, tail_out,
+                               tail);
+        } else {
+            hipLaunchKernelGGL(convert_vec_kernel<false>, dim3(blocks), dim3(256), 0, s,
+                               reinterpret_cast<const f32x4*>(in), static_cast<u16x4*>(out), groups, tail_in, tail_out,
+                               tail);
+        }
+        return hipGetLastError();
+    }
     const unsigned blocks = static_cast<unsigned>(std::max<std::size_t>(1, std::min<std::size_t>((count + 255) / 256, 8192)));
-    hipLaunchKernelGGL(convert_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), in,
-                       static_cast<unsigned short*>(out), count, dtype == MCHIP_DTYPE_BF16 ? 1 : 0);
+    hipLaunchKernelGGL(convert_kernel, dim3(blocks), dim3(256), 0, s, in, static_cast<unsigned short*>(out), count,
+                       dtype == MCHIP_DTYPE_BF16 ? 1 : 0);
     return hipGetLastError();
 }

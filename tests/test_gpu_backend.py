@@ -212,15 +212,19 @@ def test_benchmark_graphs_match_the_cpu_oracle_fused_and_unfused(device, mc, ora
         assert_close(gpu[0], cpu0[0], 1e-5, 1e-5 * max(1.0, max_abs(cpu0[0])), f"{name} vs unoptimised")
 
 
-def test_random_graphs_match_the_cpu_oracle(device, mc, oracle):
-    # tests/test_cuda_backend.cpp:399-419: 1e-4 of each output's magnitude.
-    seeds = list(range(1, 61))
+@pytest.mark.parametrize("first", [1, 51, 101, 151])
+def test_random_graphs_match_the_cpu_oracle(device, mc, oracle, first):
+    # tests/test_cuda_backend.cpp:418-437: seeds 1..200 (here in four runs of
+    # 50), 1e-4 of each output's magnitude.
+    seeds = list(range(first, first + 50))
+    print(f"case random graphs seeds {first}..{first + 49}", flush=True)
 
     def build(seed):
         text = make_random_graph(seed, 24)
         return seed, [(p, mc.Compiled(text, passes=p)) for p in ("none", "default")]
 
-    with futures.ThreadPoolExecutor(max_workers=8) as pool:
+    # hipRTC builds outside the kernel cache's lock; 16 threads, the GPU box's CPU share.
+    with futures.ThreadPoolExecutor(max_workers=16) as pool:
         compiled = list(pool.map(build, seeds))
     for seed, pairs in compiled:
         for passes, c in pairs:

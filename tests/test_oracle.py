@@ -197,3 +197,22 @@ def test_bf16_and_f16_rounding_known_answers(oracle):
     # fp16: spacing at 1 is 2^-10.
     h = oracle.round_f16(np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 65520.0, 2 ** -25], dtype=np.float32))
     assert h[0] == 1.0 and h[1] == 1 + 2 ** -9 and np.isinf(h[2]) and h[3] == 0.0
+
+
+def test_random_graphs_match_the_double_precision_evaluator(mc, oracle):
+    # CpuBackend.RandomGraphsMatchReference (tests/test_cpu_backend.cpp:176-191):
+    # the fp32 restatement against the float64 evaluator (every node rounded
+    # to float) on 200 unoptimised random graphs, 1e-4 of each output's
+    # largest magnitude.
+    from graphgen import make_random_graph
+
+    for seed in range(1, 201):
+        c = mc.Compiled(make_random_graph(seed), passes="none", backend="none")
+        inputs = [oracle.uniform(n, seed + k, -1.0, 1.0) for k, n in enumerate(c.input_sizes)]
+        actual = oracle.evaluate_compiled(c, inputs, mode="cpu")
+        expected = oracle.evaluate_compiled(c, inputs, mode="reference")
+        assert len(actual) == len(expected)
+        for k, (a, e) in enumerate(zip(actual, expected)):
+            scale = max(1.0, float(np.max(np.abs(e))) if e.size else 1.0)
+            assert np.all(np.abs(a.astype(np.float64) - e) <= 1e-4 * np.abs(e) + 1e-4 * scale), (seed, k)
+        c.close()

@@ -189,8 +189,8 @@ def test_memory_plan_known_answers(mc):
 
 
 def test_shared_buffers_never_hold_two_live_values_on_random_graphs(mc):
-    # test_memory_plan.cpp:125-146.
-    for seed in range(1, 201):
+    # test_memory_plan.cpp:125-146 (400 seeds, both output modes).
+    for seed in range(1, 401):
         c = compile_none(mc, make_random_graph(seed // 2 + 1, 24), passes="none")
         g = c.graph()
         pool = seed % 2 == 0
@@ -214,7 +214,7 @@ def test_optimized_graphs_compute_what_unoptimized_ones_do(mc, oracle):
     # fusion evaluates per element, nothing reassociates.
     removed = 0
     fused = 0
-    for seed in range(1, 121):
+    for seed in range(1, 301):
         text = make_random_graph(seed, 24)
         ref = compile_none(mc, text, passes="none")
         opt = compile_none(mc, text, passes="default")
@@ -225,7 +225,7 @@ def test_optimized_graphs_compute_what_unoptimized_ones_do(mc, oracle):
         actual = oracle.evaluate_compiled(opt, inputs)
         for k, (a, e) in enumerate(zip(actual, expected)):
             assert_close(a, e, 1e-5, 1e-5 * max(1.0, max_abs(e)), f"seed {seed} output {k}")
-    assert removed > 300 and fused > 60
+    assert removed > 1000 and fused > 150  # the reference's bound on removals: test_end_to_end.cpp:135
 
 
 @pytest.mark.parametrize("name,dims", [("gelu_chain", {"M": 64, "N": 300}),

@@ -32,6 +32,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -49,6 +50,9 @@ MALL_BYTES = 256 << 20
 # Warm-up time of every configuration other than the headline step (which
 # runs exactly --warmup untimed steps).
 WARM_SECONDS = 0.3
+# Per-launch and per-GEMM timings are the median of this many runs (their range
+# is reported beside them); the headline step time is one run of K steps.
+RUNS = 3
 
 
 def log(msg: str) -> None:
@@ -111,7 +115,8 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     steps timed between one pair of HIP events on the executable's stream
     (ms_per_step). Then each launch of the step alone, `reps` times back to
     back between one pair of HIP events on that stream (its mean duration,
-    with no event between launches to perturb it). `rotations`: list of
+    with no event between launches to perturb it), in RUNS runs: the median
+    run, and the range. `rotations`: list of
     (input_ptrs, output_ptrs) bound in turn, so consecutive launches touch
     different buffers (defeats the 256 MB MALL)."""
     def bind(i):
@@ -144,21 +149,25 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_ms(stop)
     reps = reps or max(steps, 10)
-    launch_ms = []
+    launch_ms, launch_range = [], []
     for j in range(compiled.kernel_launches):
         for i in range(2):
             bind(i)
             compiled.enqueue_launch(j)
-        start.record(stream)
-        for i in range(reps):
-            bind(i)
-            compiled.enqueue_launch(j)
-        stop.record(stream)
-        compiled.synchronize()
-        launch_ms.append(start.elapsed_ms(stop) / reps)
+        runs = []
+        for _ in range(RUNS):
+            start.record(stream)
+            for i in range(reps):
+                bind(i)
+                compiled.enqueue_launch(j)
+            stop.record(stream)
+            compiled.synchronize()
+            runs.append(start.elapsed_ms(stop) / reps)
+        launch_ms.append(statistics.median(runs))
+        launch_range.append([min(runs), max(runs)])
     bind(0)
     return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "launch_ms": launch_ms,
-            "launch_reps": reps}
+            "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS}
 
 
 def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0) -> dict:
@@ -169,6 +178,8 @@ def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_second
     work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
+    for e, r in zip(kernels, t["launch_ms_range"]):
+        e["ms_range"] = r
     flop = sum(w["flop"] for w in work if w["kind"] == "gemm")
     return {"compiled": c, "timing": t, "kernels": kernels, "gemm_flop": flop,
             "value": flop / (t["ms_per_step"] * 1e-3) / 1e12, "jit_ms": c.jit_compile_ms}
@@ -190,14 +201,17 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
     t = time_graph(mc, c, steps, warmup, rot, warm_seconds=WARM_SECONDS)
     work = node_work(c.graph(), c.launch_nodes)
     (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
+    k["ms_range"] = t["launch_ms_range"][0]
+    k["gbs_range"] = [k["bytes"] / (ms * 1e-3) / 1e9 for ms in reversed(k["ms_range"])]
     return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
             "gbs": k["gbs"], "frac": k["frac"]}
 
 
-def time_gemm(mc, launch, steps: int, warmup: int) -> float:
+def time_gemm(mc, launch, steps: int, warmup: int, runs_out: list | None = None) -> float:
     """Mean duration of `steps` back-to-back launches between one pair of HIP
     events on their stream, after `warmup` launches and a warm-up of
-    WARM_SECONDS."""
+    WARM_SECONDS; the median of RUNS such runs (each run's figure appended
+    to `runs_out`)."""
     s = mc.Stream()
     for _ in range(warmup):
         launch(s)
@@ -209,12 +223,17 @@ def time_gemm(mc, launch, steps: int, warmup: int) -> float:
 
     warm_up_for(WARM_SECONDS, extra)
     start, stop = mc.Event(), mc.Event()
-    start.record(s)
-    for _ in range(steps):
-        launch(s)
-    stop.record(s)
-    s.synchronize()
-    return start.elapsed_ms(stop) / steps
+    runs = []
+    for _ in range(RUNS):
+        start.record(s)
+        for _ in range(steps):
+            launch(s)
+        stop.record(s)
+        s.synchronize()
+        runs.append(start.elapsed_ms(stop) / steps)
+    if runs_out is not None:
+        runs_out.extend(runs)
+    return statistics.median(runs)
 
 
 def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]:
@@ -227,10 +246,11 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
         c = mc.DeviceBuffer(4 * m * n)
         ws_bytes = mc.matmul_workspace_bytes(kernel, m, n, splits)
         ws = mc.DeviceBuffer(ws_bytes) if ws_bytes else None
+        runs = []
         ms = time_gemm(mc, lambda s: mc.launch_matmul(kernel, a.ptr, b.ptr, c.ptr, m, n, k, s, splits,
-                                                       ws.ptr if ws else None), steps, warmup)
+                                                       ws.ptr if ws else None), steps, warmup, runs)
         flop = 2.0 * m * n * k
-        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "ms": ms,
+        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "ms": ms, "ms_range": [min(runs), max(runs)],
              "tflops": flop / (ms * 1e-3) / 1e12}
         e["frac"] = e["tflops"] / PEAK_FP32_TFLOPS
         if m == 16:  # HBM-bound skinny shape: report bytes too
@@ -252,11 +272,12 @@ def bench_gemm_lowp(mc, shapes, steps: int, warmup: int) -> list[dict]:
             mc.convert_f32(dtype, a32.ptr, a.ptr, m * k)
             mc.convert_f32(dtype, b32.ptr, b.ptr, k * n)
             c = mc.DeviceBuffer(4 * m * n)
+            runs = []
             ms = time_gemm(mc, lambda s: mc.launch_matmul_lowp(kernel, dtype, a.ptr, b.ptr, c.ptr, m, n, k, s),
-                           steps, warmup)
+                           steps, warmup, runs)
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
             out.append({"m": m, "n": n, "k": k, "kernel": kernel, "inputs": "bf16" if dtype == 1 else "fp16",
-                        "ms": ms, "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
+                        "ms": ms, "ms_range": [min(runs), max(runs)], "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
             log(f"gemm {kernel} {m}x{n}x{k}: {ms:.3f} ms {tf:.1f} TFLOP/s")
             del a, b, c
     return out

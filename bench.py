@@ -433,18 +433,20 @@ def main() -> int:
                          "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
     if args.workload == "mlp" and not args.quick:
-        # BASELINE config 2's batch sweep: the small batches are launch-bound,
-        # so each is timed with direct launches and with hipGraph replay.
+        # BASELINE config 2's batch sweep: the small batches are timed with
+        # direct launches, with hipGraph replay, and with the split count and
+        # tile configuration autotuned at compile time (autotune=1).
         cfgs = line.setdefault("configs", {})
         for b in (256, 1024):
             entry = {}
-            for mode, opts in (("direct", None), ("graph_replay", {"graph": 1})):
+            for mode, opts in (("direct", None), ("graph_replay", {"graph": 1}), ("autotuned", {"autotune": 1})):
                 r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts, WARM_SECONDS)
                 entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
                                "launches": r["compiled"].kernel_launches}
             cfgs[f"mlp_b{b}"] = entry
             log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
-                f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step")
+                f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step, "
+                f"autotuned {entry['autotuned']['ms_per_step'] * 1e3:.1f} us/step")
     if args.workload == "gemm_fp32" or (args.workload == "mlp" and not args.quick):
         shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384), (16, 4096, 4096)]
         g = bench_gemm_fp32(mc, cus, shapes, 10, 3)  # plus WARM_SECONDS per shape

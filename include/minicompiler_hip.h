@@ -160,6 +160,15 @@ MC_API int mc_compile_kernel_source(const char* source, const char* arch, char* 
  * 1, `workspace` (mc_matmul_workspace_bytes). Returns a hipError_t value. */
 MC_API int mc_launch_matmul(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
                             int splits, float* workspace);
+/* mc_launch_matmul for double_buffered / split_k with the FP32 ring
+ * configuration forced (no counterpart in the reference, whose tiles are
+ * fixed; the autotuner picks one, see the `autotune` option): ring_cfg 0 =
+ * the planner's own, 1 = wide (128x128 tiles), 2 = mid (64x128), 3 = big
+ * (256x256), 4 = thin (32x128). The configuration does not change the bits.
+ * hipErrorInvalidValue when it cannot run the product (K not a multiple of
+ * 32, N not of 4, operands not 16-byte aligned) or for other kernels. */
+MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                void* stream, int splits, float* workspace, int ring_cfg);
 /* The matrix-core kernels on inputs already stored as bf16 (dtype 1) or fp16
  * (dtype 2); fp32 accumulation and output. */
 MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,

@@ -98,6 +98,7 @@ _SIGNATURES = {
     "mc_compile_kernel_source": (_i, [_cp, _cp, _cp, _i]),
     "mc_generate_gemm_epilogue_kernel": (_i, [_cp, _i, _cp, _cp, _i, _cp, _i]),
     "mc_launch_matmul": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "mc_launch_matmul_cfg": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _i]),
     "mc_launch_matmul_lowp": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "mc_convert_f32": (_i, [_i, _vp, _vp, _sz, _vp]),
     "mc_sum_split_partials": (_i, [_vp, _vp, _sz, _i, _vp]),
@@ -519,6 +520,18 @@ def launch_matmul(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: 
     kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
     _check(library().mc_launch_matmul(kid, a, b, c, m, n, k, _stream_handle(stream), splits, workspace),
            f"launch_matmul({matmul_kernel_name(kid)})")
+
+
+RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4}
+
+
+def launch_matmul_cfg(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: int, stream=None,
+                      splits: int = 1, workspace: int | None = None, ring: int | str = "auto") -> None:
+    """launch_matmul with the FP32 ring configuration forced (RING_CONFIGS)."""
+    kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
+    cfg = RING_CONFIGS[ring] if isinstance(ring, str) else ring
+    _check(library().mc_launch_matmul_cfg(kid, a, b, c, m, n, k, _stream_handle(stream), splits, workspace, cfg),
+           f"launch_matmul_cfg({matmul_kernel_name(kid)}, ring {ring})")
 
 
 def launch_matmul_lowp(kernel: int | str, dtype: int, a: int, b: int, c: int, m: int, n: int, k: int, stream=None,

@@ -725,6 +725,11 @@ MC_API int mc_launch_matmul(int kernel, const float* a, const float* b, float* c
     return mchip_launch_matmul(kernel, a, b, c, m, n, k, stream, splits, workspace);
 }
 
+MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                void* stream, int splits, float* workspace, int ring_cfg) {
+    return mchip_launch_matmul_cfg(kernel, a, b, c, m, n, k, stream, splits, workspace, ring_cfg);
+}
+
 MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,
                                  void* stream, int splits, float* workspace) {
     return mchip_launch_matmul_lowp(kernel, dtype, a, b, c, m, n, k, stream, splits, workspace);

@@ -21,12 +21,12 @@ namespace {
 
 constexpr std::size_t kMaxWorkspace = std::size_t{512} << 20;
 
-// (device tag, m, n, k) -> splits.
+// (device tag, m, n, k) -> choice.
 using Key = std::tuple<std::string, int, int, int>;
 
 struct Decisions {
     std::mutex mu;
-    std::map<Key, int> splits;
+    std::map<Key, Fp32Choice> choice;
     std::set<std::string> loaded;  // device tags whose file has been read
 };
 
@@ -54,8 +54,8 @@ std::string decisions_file(const std::string& tag) {
     return std::string(dir) + "/autotune_" + tag + ".txt";
 }
 
-// The file holds one decision per line: "m n k splits". Lines that do not
-// parse, or name a split count outside the candidates, are ignored.
+// The file holds one decision per line: "m n k splits ring_cfg". Lines
+// that do not parse, or name a choice outside the candidates, are ignored.
 void load_file(Decisions& d, const std::string& tag, int cu_count) {
     if (!d.loaded.insert(tag).second) return;
     const std::string path = decisions_file(tag);
@@ -64,19 +64,20 @@ void load_file(Decisions& d, const std::string& tag, int cu_count) {
     std::string line;
     while (std::getline(f, line)) {
         std::istringstream s(line);
-        int m = 0, n = 0, k = 0, splits = 0;
-        if (!(s >> m >> n >> k >> splits) || m < 1 || n < 1 || k < 1) continue;
-        const std::vector<int> c = autotune_candidates(m, n, k, cu_count);
-        if (std::find(c.begin(), c.end(), splits) == c.end()) continue;
-        d.splits[Key{tag, m, n, k}] = splits;
+        int m = 0, n = 0, k = 0;
+        Fp32Choice c;
+        if (!(s >> m >> n >> k >> c.splits >> c.ring_cfg) || m < 1 || n < 1 || k < 1) continue;
+        const std::vector<Fp32Choice> cands = autotune_candidates(m, n, k, cu_count);
+        if (std::find(cands.begin(), cands.end(), c) == cands.end()) continue;
+        d.choice[Key{tag, m, n, k}] = c;
     }
 }
 
-void append_file(const std::string& tag, int m, int n, int k, int splits) {
+void append_file(const std::string& tag, int m, int n, int k, const Fp32Choice& c) {
     const std::string path = decisions_file(tag);
     if (path.empty()) return;
     std::ofstream f(path, std::ios::app);
-    if (f) f << m << ' ' << n << ' ' << k << ' ' << splits << '\n';
+    if (f) f << m << ' ' << n << ' ' << k << ' ' << c.splits << ' ' << c.ring_cfg << '\n';
 }
 
 struct DeviceMem {
@@ -111,10 +112,10 @@ Status hip_status(int rc, const char* what) {
         if (!st_.ok()) return st_.error();                  \
     } while (0)
 
-Result<int> time_candidates(int m, int n, int k, const std::vector<int>& cands) {
+Result<Fp32Choice> time_candidates(int m, int n, int k, const std::vector<Fp32Choice>& cands) {
     const std::size_t mn = static_cast<std::size_t>(m) * n;
     int max_split = 1;
-    for (int s : cands) max_split = std::max(max_split, s);
+    for (const Fp32Choice& c : cands) max_split = std::max(max_split, c.splits);
     DeviceMem a, b, c, ws;
     Resources r;
     MC_AT_TRY(mchip_malloc(&a.p, static_cast<std::size_t>(m) * k * 4));
@@ -129,13 +130,14 @@ Result<int> time_candidates(int m, int n, int k, const std::vector<int>& cands) 
     MC_AT_TRY(mchip_memset_async(a.p, 0x3c, static_cast<std::size_t>(m) * k * 4, r.stream));
     MC_AT_TRY(mchip_memset_async(b.p, 0x3c, static_cast<std::size_t>(k) * n * 4, r.stream));
 
-    auto launch = [&](int s) {
+    auto launch = [&](const Fp32Choice& ch) {
+        const int s = ch.splits;
         const MatmulKernel kernel = s > 1 ? MatmulKernel::SplitK : MatmulKernel::DoubleBuffered;
-        return mchip_launch_matmul(static_cast<int>(kernel), static_cast<const float*>(a.p),
-                                   static_cast<const float*>(b.p), static_cast<float*>(c.p), m, n, k, r.stream, s,
-                                   s > 1 ? static_cast<float*>(ws.p) : nullptr);
+        return mchip_launch_matmul_cfg(static_cast<int>(kernel), static_cast<const float*>(a.p),
+                                       static_cast<const float*>(b.p), static_cast<float*>(c.p), m, n, k, r.stream, s,
+                                       s > 1 ? static_cast<float*>(ws.p) : nullptr, ch.ring_cfg);
     };
-    auto time_reps = [&](int s, int reps, double* ms) -> Status {
+    auto time_reps = [&](const Fp32Choice& s, int reps, double* ms) -> Status {
         MC_AT_TRY(launch(s));
         MC_AT_TRY(mchip_event_record(r.start, r.stream));
         for (int i = 0; i < reps; ++i) MC_AT_TRY(launch(s));
@@ -151,7 +153,7 @@ Result<int> time_candidates(int m, int n, int k, const std::vector<int>& cands) 
     // milliseconds), and the first candidates would otherwise be timed cold.
     const auto until = std::chrono::steady_clock::now() + std::chrono::milliseconds(40);
     while (std::chrono::steady_clock::now() < until) {
-        for (int s : cands) MC_AT_TRY(launch(s));
+        for (const Fp32Choice& s : cands) MC_AT_TRY(launch(s));
         MC_AT_TRY(mchip_stream_synchronize(r.stream));
     }
     // About a millisecond of launches per timing, best of three rounds.
@@ -171,8 +173,8 @@ Result<int> time_candidates(int m, int n, int k, const std::vector<int>& cands) 
             best[i] = std::min(best[i], ms);
         }
     }
-    // Candidates are in increasing split order; a larger split has to be more
-    // than 2% faster than the best smaller one to be chosen.
+    // The default comes first; another candidate has to be more than 2%
+    // faster than the best before it to be chosen.
     std::size_t pick = 0;
     for (std::size_t i = 1; i < cands.size(); ++i) {
         if (best[i] < 0.98 * best[pick]) pick = i;
@@ -182,40 +184,41 @@ Result<int> time_candidates(int m, int n, int k, const std::vector<int>& cands) 
 
 }  // namespace
 
-std::vector<int> autotune_candidates(int m, int n, int k, int cu_count) {
-    std::vector<int> out{1};
-    if (m < 1 || n < 1 || k < 1 || cu_count < 1) return out;
-    const std::int64_t tiles = ((static_cast<std::int64_t>(m) + kSplitTileM - 1) / kSplitTileM) *
-                               ((static_cast<std::int64_t>(n) + kSplitTileN - 1) / kSplitTileN);
+std::vector<Fp32Choice> autotune_candidates(int m, int n, int k, int cu_count) {
+    const int rule = m >= 1 && n >= 1 && k >= 1 && cu_count >= 1 ? split_k_splits(m, n, k, cu_count) : 1;
+    std::vector<Fp32Choice> out{Fp32Choice{std::max(rule, 1), MCHIP_RING_NONE}};
+    if (m < 1 || n < 1 || k < 1 || cu_count < 1 || k % 32 != 0 || n % 4 != 0) return out;
+    auto tiles = [&](std::int64_t bm, std::int64_t bn) {
+        return ((static_cast<std::int64_t>(m) + bm - 1) / bm) * ((static_cast<std::int64_t>(n) + bn - 1) / bn);
+    };
+    if (tiles(kSplitTileM, kSplitTileN) >= 2LL * cu_count) return out;
     const std::int64_t mn = static_cast<std::int64_t>(m) * n;
-    const int rule = split_k_splits(m, n, k, cu_count);
-    if (tiles < 2LL * cu_count) {
-        for (int s = 2; s <= 64; s *= 2) {
-            if (s > k / 64 || tiles * s > 4LL * cu_count) break;
-            if (static_cast<std::size_t>(s) * static_cast<std::size_t>(mn) * 4 > kMaxWorkspace) break;
-            out.push_back(s);
+    const struct { int cfg; std::int64_t bm, bn; } cfgs[] = {
+        {MCHIP_RING_WIDE, 128, 128}, {MCHIP_RING_MID, 64, 128}, {MCHIP_RING_THIN, 32, 128}};
+    for (const auto& c : cfgs) {
+        const std::int64_t t = tiles(c.bm, c.bn);
+        for (int s = 1; s <= 64; s *= 2) {
+            if (s > 1 && (s > k / 64 || t * s > 4LL * cu_count)) break;
+            if (s > 1 && static_cast<std::size_t>(s) * static_cast<std::size_t>(mn) * 4 > kMaxWorkspace) break;
+            const Fp32Choice ch{s, c.cfg};
+            if (std::find(out.begin(), out.end(), ch) == out.end()) out.push_back(ch);
         }
     }
-    if (rule > 1 && std::find(out.begin(), out.end(), rule) == out.end() &&
-        static_cast<std::size_t>(rule) * static_cast<std::size_t>(mn) * 4 <= kMaxWorkspace) {
-        out.push_back(rule);
-    }
-    std::sort(out.begin(), out.end());
     return out;
 }
 
-Result<int> autotune_fp32_splits(const DeviceInfo& device, int m, int n, int k) {
-    const std::vector<int> cands = autotune_candidates(m, n, k, device.cu_count);
+Result<Fp32Choice> autotune_fp32(const DeviceInfo& device, int m, int n, int k) {
+    const std::vector<Fp32Choice> cands = autotune_candidates(m, n, k, device.cu_count);
     if (cands.size() == 1) return cands[0];
     const std::string tag = device_tag(device);
     Decisions& d = decisions();
     std::lock_guard<std::mutex> lock(d.mu);
     load_file(d, tag, device.cu_count);
     const Key key{tag, m, n, k};
-    if (auto it = d.splits.find(key); it != d.splits.end()) return it->second;
-    Result<int> chosen = time_candidates(m, n, k, cands);
+    if (auto it = d.choice.find(key); it != d.choice.end()) return it->second;
+    Result<Fp32Choice> chosen = time_candidates(m, n, k, cands);
     if (!chosen.ok()) return chosen.error();
-    d.splits[key] = chosen.value();
+    d.choice[key] = chosen.value();
     append_file(tag, m, n, k, chosen.value());
     return chosen.value();
 }
@@ -223,7 +226,7 @@ Result<int> autotune_fp32_splits(const DeviceInfo& device, int m, int n, int k) 
 std::size_t autotune_cached_decisions() {
     Decisions& d = decisions();
     std::lock_guard<std::mutex> lock(d.mu);
-    return d.splits.size();
+    return d.choice.size();
 }
 
 }  // namespace minicompiler::hip

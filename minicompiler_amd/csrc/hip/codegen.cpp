@@ -219,6 +219,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
     } else {
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"
                           : body == GemmBody::F32RingThin ? "McRingThin"
+                          : body == GemmBody::F32RingMid  ? "McRingMid"
                                                           : "McRingWide";
         os << "\tmc_gemm_f32_ring<" << cfg << ">(a, b, c, "
            << mnk << ", " << split << ", partial, epi);\n}\n\n";

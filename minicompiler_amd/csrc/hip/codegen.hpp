@@ -75,14 +75,15 @@ enum class GemmBody {
     F32Mfma,      // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K (gemm_f32_mfma.h)
     F32RingBig,   // the same arithmetic, LDS ring, persistent (gemm_f32_ring.h): 256x256 tiles, one block per CU
     F32RingWide,  // likewise, 128x128 tiles, 2 stages, up to two blocks per CU
-    F32RingThin,  // likewise, 32x128 tiles (M <= 32), 6 stages
+    F32RingThin,  // likewise, 32x128 tiles (M <= 32, or when the autotuner picks it), 6 stages
+    F32RingMid,   // likewise, 64x128 tiles, 3 stages, up to two blocks per CU (autotuner only)
     Bf16Fast,     // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
     F16Fast,      // fp16 operands, likewise
 };
 
 inline bool is_f32_body(GemmBody body) {
     return body == GemmBody::F32Mfma || body == GemmBody::F32RingBig || body == GemmBody::F32RingWide ||
-           body == GemmBody::F32RingThin;
+           body == GemmBody::F32RingThin || body == GemmBody::F32RingMid;
 }
 
 // A GEMM (the matrix-core body in `gemm_body_source`, of kind `body`) whose

@@ -88,10 +88,15 @@ struct McRingCfg {
 //         direct fetch instruction holds up the wave's MFMA issue);
 //   thin: for M <= 32 (HBM-bound on B): 32x128 tiles, 4 waves of 32x32, 6
 //         stages of 20 KiB keeping more of B in flight, so a 128-row tile's
-//         MFMA work on clamped rows no longer dominates.
+//         MFMA work on clamped rows no longer dominates;
+//   mid:  64x128 tiles, 4 waves of 32x64, 3 stages of 24 KiB, up to two
+//         blocks per CU. Chosen only by the autotuner (with thin at any M):
+//         small products split K less with smaller tiles (1024 x 2048 x 512
+//         unsplit on mid: 23.8 us against 31.4 us for wide with 2 splits).
 using McRingBig = McRingCfg<256, 256, 128, 128, 4, 2>;
 using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2, true>;
 using McRingThin = McRingCfg<32, 128, 32, 32, 4, 6>;
+using McRingMid = McRingCfg<64, 128, 32, 64, 4, 3>;
 
 // LDS layout of a stage (bytes):
 //   A at 0: kBM / 8 blocks of 1 KiB, block rb holding rows 8 rb .. 8 rb + 7

@@ -67,6 +67,7 @@ struct Launch {
     // Matmul.
     MatmulKernel matmul = MatmulKernel::DoubleBuffered;
     int splits = 1;
+    int ring_cfg = 0;  // MCHIP_RING_*: forced FP32 ring configuration (0: the planner's)
     float* workspace = nullptr;
     int m = 0, n = 0, k = 0;
     // FusedMatmul: generated kernels and their stable arguments.
@@ -448,10 +449,16 @@ private:
             }
             return Status();
         }
-        const int rc = mchip_launch_matmul(static_cast<int>(l.matmul), static_cast<const float*>(value_ptr(a_of(l))),
-                                           static_cast<const float*>(value_ptr(b_of(l))),
-                                           static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, l.splits,
-                                           l.workspace);
+        const void* pa = value_ptr(a_of(l));
+        const void* pb = value_ptr(b_of(l));
+        void* pc = value_ptr(l.node);
+        // A tuned ring configuration needs 16-byte aligned operands (bound
+        // caller buffers may not be); the planner's own choice runs any.
+        const bool aligned = ((reinterpret_cast<std::uintptr_t>(pa) | reinterpret_cast<std::uintptr_t>(pb) |
+                               reinterpret_cast<std::uintptr_t>(pc)) & 15u) == 0;
+        const int rc = mchip_launch_matmul_cfg(static_cast<int>(l.matmul), static_cast<const float*>(pa),
+                                               static_cast<const float*>(pb), static_cast<float*>(pc), l.m, l.n, l.k,
+                                               s, l.splits, l.workspace, aligned ? l.ring_cfg : 0);
         if (rc != 0) {
             return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " + mchip_error_string(rc)};
         }
@@ -487,11 +494,13 @@ private:
         }
         l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
         if (options_.autotune && options_.matmul == MatmulKernel::Auto) {
-            // The split count timed on this device (double_buffered unsplit,
-            // split_k otherwise) instead of the split rule's.
-            Result<int> tuned = autotune_fp32_splits(device_, l->m, l->n, l->k);
+            // The split count and ring configuration timed on this device
+            // (double_buffered unsplit, split_k otherwise) instead of the
+            // split rule's count and the planner's configuration.
+            Result<Fp32Choice> tuned = autotune_fp32(device_, l->m, l->n, l->k);
             if (!tuned.ok()) return tuned.error();
-            l->splits = tuned.value();
+            l->splits = tuned->splits;
+            l->ring_cfg = tuned->ring_cfg;
             l->matmul = l->splits > 1 ? MatmulKernel::SplitK : MatmulKernel::DoubleBuffered;
         }
         const bool bf16 = l->matmul == MatmulKernel::TensorCoreBf16, f16 = l->matmul == MatmulKernel::TensorCoreF16;
@@ -513,10 +522,11 @@ private:
         split_layout(l.k, l.splits, &l.k_split, &l.depth);
         if (l.matmul == MatmulKernel::Vectorized || l.k % 4 != 0) return GemmBody::F32Mfma;
         unsigned grid = 0, block = 0;
-        switch (mchip_f32_ring_plan(l.m, l.n, l.k, l.depth, device_.cu_count, &grid, &block)) {
+        switch (mchip_f32_ring_plan_cfg(l.m, l.n, l.k, l.depth, device_.cu_count, l.ring_cfg, &grid, &block)) {
             case MCHIP_RING_BIG: return GemmBody::F32RingBig;
             case MCHIP_RING_THIN: return GemmBody::F32RingThin;
             case MCHIP_RING_WIDE: return GemmBody::F32RingWide;
+            case MCHIP_RING_MID: return GemmBody::F32RingMid;
             default: return GemmBody::F32Mfma;
         }
     }
@@ -656,7 +666,7 @@ private:
                     l.block = 256;
                 } else {
                     unsigned grid = 0, block = 0;
-                    mchip_f32_ring_plan(l.m, l.n, l.k, l.depth, device_.cu_count, &grid, &block);
+                    mchip_f32_ring_plan_cfg(l.m, l.n, l.k, l.depth, device_.cu_count, l.ring_cfg, &grid, &block);
                     l.grid_x = grid;
                     l.grid_y = l.grid_z = 1;
                     l.block = block;

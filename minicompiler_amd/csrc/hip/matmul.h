@@ -53,9 +53,21 @@ int mchip_matmul_blocks_per_cu(int kernel);
  *   MCHIP_RING_THIN  for m <= 32: 32x128 tiles, 6 LDS stages.
  * The choice minimises (rounds of tiles per CU) x (work per tile) / (the
  * configuration's measured efficiency). *grid receives the number of
- * blocks, *block the lanes per block. */
-enum { MCHIP_RING_NONE = 0, MCHIP_RING_WIDE = 1, MCHIP_RING_BIG = 3, MCHIP_RING_THIN = 4 };
+ * blocks, *block the lanes per block.
+ *   MCHIP_RING_MID   64x128 tiles, up to two blocks per CU: never chosen
+ *                    here, only when forced (the autotuner times it).
+ * mchip_f32_ring_plan_cfg with cfg != MCHIP_RING_NONE forces that
+ * configuration (thin then at any m), if the shape fits the ring at all. */
+enum { MCHIP_RING_NONE = 0, MCHIP_RING_WIDE = 1, MCHIP_RING_MID = 2, MCHIP_RING_BIG = 3, MCHIP_RING_THIN = 4 };
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
+int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);
+
+/* mchip_launch_matmul with the ring configuration forced (MCHIP_RING_NONE:
+ * the plan's own) for double_buffered and split_k; hipErrorInvalidValue
+ * when that configuration cannot run the product (K not a multiple of 32, N
+ * not of 4, operands not 16-byte aligned) or for other kernels. */
+int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
+                            int splits, float* workspace, int ring_cfg);
 
 /* Elementwise fp32 -> bf16/fp16 (round to nearest even), for staging. */
 int mchip_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream);

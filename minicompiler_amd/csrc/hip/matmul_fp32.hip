@@ -158,6 +158,7 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
 using RingBig = McRingBig;
 using RingWide = McRingWide;
 using RingThin = McRingThin;
+using RingMid = McRingMid;
 constexpr int kRBKRing = RingWide::kBK;
 
 template <class Cfg, int kBlocksPerCu>
@@ -213,7 +214,7 @@ int device_cu_count() {
 }
 
 int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
-                    hipStream_t stream, int splits, float* workspace) {
+                    hipStream_t stream, int splits, float* workspace, int ring_cfg) {
     const int k_split = split_len(k, splits, kMBK);
     const int depth = std::max(1, (k + k_split - 1) / k_split);
     if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
@@ -222,8 +223,9 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     float* out_ws = depth > 1 ? workspace : nullptr;
     unsigned ring_grid = 0, ring_block = 0;
     const int ring = double_buffer && vec && aligned16(c)
-                         ? mchip_f32_ring_plan(m, n, k, depth, device_cu_count(), &ring_grid, &ring_block)
+                         ? mchip_f32_ring_plan_cfg(m, n, k, depth, device_cu_count(), ring_cfg, &ring_grid, &ring_block)
                          : MCHIP_RING_NONE;
+    if (ring_cfg != MCHIP_RING_NONE && ring != ring_cfg) return hipErrorInvalidValue;
     if (ring == MCHIP_RING_THIN) {
         hipLaunchKernelGGL((matmul_ring_f32<RingThin, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws);
@@ -232,6 +234,9 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
                            k, k_split, depth, out_ws);
     } else if (ring == MCHIP_RING_WIDE) {
         hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws);
+    } else if (ring == MCHIP_RING_MID) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingMid, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws);
     } else if (double_buffer) {
         if (vec) {
@@ -253,11 +258,29 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
 
 }  // namespace
 
-extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block) {
+extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid,
+                                       unsigned* block) {
     *grid = 0;
     *block = 0;
     if (m < 1 || n < 4 || k < kRBKRing || k % kRBKRing != 0 || n % 4 != 0 || depth < 1 || cu_count < 1) {
         return MCHIP_RING_NONE;
+    }
+    if (cfg != MCHIP_RING_NONE) {
+        // A forced configuration: its tiles, in persistent blocks (at most
+        // one per CU for big and thin, two for wide and mid).
+        long long bm = 0, bn = 0, per_cu = 1;
+        unsigned threads = 0;
+        switch (cfg) {
+            case MCHIP_RING_BIG: bm = RingBig::kBM, bn = RingBig::kBN, threads = RingBig::kThreads; break;
+            case MCHIP_RING_WIDE: bm = RingWide::kBM, bn = RingWide::kBN, threads = RingWide::kThreads, per_cu = 2; break;
+            case MCHIP_RING_MID: bm = RingMid::kBM, bn = RingMid::kBN, threads = RingMid::kThreads, per_cu = 2; break;
+            case MCHIP_RING_THIN: bm = RingThin::kBM, bn = RingThin::kBN, threads = RingThin::kThreads; break;
+            default: return MCHIP_RING_NONE;
+        }
+        const long long units = ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * depth;
+        *grid = static_cast<unsigned>(std::min(units, per_cu * cu_count));
+        *block = threads;
+        return cfg;
     }
     // Time in units of one 128x128 tile-split on a whole CU: the tile-splits
     // of the busiest CU x work per tile-split (a 256x256 tile is four) /
@@ -284,6 +307,10 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     *grid = static_cast<unsigned>(wide_grid);
     *block = RingWide::kThreads;
     return MCHIP_RING_WIDE;
+}
+
+extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block) {
+    return mchip_f32_ring_plan_cfg(m, n, k, depth, cu_count, MCHIP_RING_NONE, grid, block);
 }
 
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
@@ -328,12 +355,24 @@ extern "C" int mchip_launch_matmul(int kernel, const float* a, const float* b, f
             hipLaunchKernelGGL((matmul_register_tiled<64, 64, 8, 4, 4>), grid, dim3(256), 0, s, a, b, c, m, n, k);
             return hipGetLastError();
         }
-        case kVectorized: return launch_mfma_f32(false, a, b, c, m, n, k, s, 1, nullptr);
-        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr);
-        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace);
+        case kVectorized: return launch_mfma_f32(false, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE);
+        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE);
+        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, MCHIP_RING_NONE);
         case kTensorCoreTf32:
         case kTensorCoreBf16:
         case kTensorCoreF16: return mchip_launch_tensor_core(kernel, a, b, c, m, n, k, stream, splits, workspace);
         default: return hipErrorInvalidValue;  // Auto must be resolved first
+    }
+}
+
+extern "C" int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                       void* stream, int splits, float* workspace, int ring_cfg) {
+    if (ring_cfg == MCHIP_RING_NONE) return mchip_launch_matmul(kernel, a, b, c, m, n, k, stream, splits, workspace);
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (kernel) {
+        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, ring_cfg);
+        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, ring_cfg);
+        default: return hipErrorInvalidValue;  // only the ring rungs take a configuration
     }
 }

@@ -1,8 +1,9 @@
-"""Compile-time autotuning of the FP32 matmul's K split (option autotune=1):
-the MLP at B=256 and B=1024 (each GEMM has fewer 128x128 tiles than two
-per CU, so several split counts are timed) matches the CPU oracle within
-the FP32 tolerance, the decisions land in MINICOMPILER_HIP_CACHE_DIR, and a
-second process reads them instead of timing and computes the same bits.
+"""Compile-time autotuning of the FP32 matmul's K split and tile
+configuration (option autotune=1): the MLP at B=256 and B=1024 (each GEMM
+has fewer 128x128 tiles than two per CU, so several split counts on wide,
+mid and thin tiles are timed) matches the CPU oracle within the FP32
+tolerance, the decisions land in MINICOMPILER_HIP_CACHE_DIR, and a second
+process reads them instead of timing and computes the same bits.
 (The reference fixes the split by a rule, src/cuda/matmul_kernels.cu:352-367;
 tuning it on the device is this build's.)"""
 
@@ -65,8 +66,13 @@ def test_autotuned_splits_stay_within_the_fp32_bound_and_are_reused(device, mc, 
     # (m, n, k) of GEMM1 (B x 2048 x 512) and GEMM2 (B x 512 x 2048).
     assert shapes == {(256, 2048, 512), (256, 512, 2048), (1024, 2048, 512), (1024, 512, 2048)}, lines
     for line in lines:
-        m, n, k, s = (int(v) for v in line.split())
-        assert s in (1, 2, 4, 8, 16, 32, 64) and s <= max(1, k // 64), line
+        # splits and ring configuration: the rule's split count on the
+        # planner's configuration (0), or a power of two on wide (1), mid (2)
+        # or thin (4) tiles.
+        m, n, k, s, cfg = (int(v) for v in line.split())
+        rule = mc.split_k_splits(m, n, k, device["cu_count"])
+        assert (cfg == 0 and s == max(rule, 1)) or (cfg in (1, 2, 4) and s in (1, 2, 4, 8, 16, 32, 64)
+                                                     and s <= max(1, k // 64)), line
     for b in (256, 1024):
         assert set(first[b]["kernels"]) <= {"double_buffered", "split_k"}
         c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": b}, backend="none")

@@ -73,3 +73,47 @@ def test_fused_epilogue_on_the_ring_equals_the_two_stage_body(device, mc, oracle
     x, y = ring.run(inputs), two.run(inputs)
     for p, q in zip(x, y):
         assert np.array_equal(p.view(np.uint32), q.view(np.uint32))
+
+
+# Every ring configuration forced (mc_launch_matmul_cfg, as the autotuner
+# launches them), unsplit and split: the same bits as the plan's own
+# configuration (each C element gets the same MFMA sequence whatever the
+# tile), and within the dot-product bound. Ragged M and N, thin and mid
+# tiles at M > 32, a single mid tile with a long K, and split counts that do
+# and do not divide K's steps evenly.
+FORCED_SHAPES = [(300, 96, 260), (1000, 512, 1028), (64, 2048, 128), (33, 256, 4100)]
+
+
+def run_cfg(mc, kernel, ring, da, db, m, n, k, splits, ws):
+    dc = mc.DeviceBuffer.from_array(np.full(m * n + GUARD, np.nan, dtype=np.float32))
+    mc.launch_matmul_cfg(kernel, da.ptr, db.ptr, dc.ptr, m, n, k, None, splits, ws.ptr if ws else None, ring)
+    mc.synchronize()
+    out = dc.download()
+    assert np.all(np.isnan(out[m * n:])), f"{ring}: a write past the end of C"
+    assert not np.any(np.isnan(out[:m * n])), f"{ring}: an element of C was not written"
+    return out[:m * n]
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("m,k,n", FORCED_SHAPES)
+def test_forced_ring_configurations_give_the_plans_bits(device, mc, oracle, m, k, n, splits):
+    print(f"case forced ring {m}x{k}x{n} splits {splits}", flush=True)
+    a = oracle.uniform(m * k, 21, -1.0, 1.0)
+    b = oracle.uniform(k * n, 22, -1.0, 1.0)
+    da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
+    kernel = "split_k" if splits > 1 else "double_buffered"
+    ws_bytes = mc.matmul_workspace_bytes(kernel, m, n, splits) if splits > 1 else 0
+    ws = mc.DeviceBuffer(ws_bytes) if ws_bytes else None
+    ref = run_cfg(mc, kernel, "auto", da, db, m, n, k, splits, ws)
+    for ring in ("wide", "mid", "big", "thin"):
+        got = run_cfg(mc, kernel, ring, da, db, m, n, k, splits, ws)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), ring
+    exact, absdot = oracle.gemm_f64(a, b, m, k, n)
+    assert np.all(np.abs(ref.astype(np.float64) - exact) <= fp32_gemm_bound(exact, absdot, k))
+
+
+def test_a_forced_configuration_the_product_cannot_take_is_an_error(device, mc):
+    # K not a multiple of 32: no ring configuration runs it.
+    da, db, dc = mc.DeviceBuffer(4 * 64 * 40), mc.DeviceBuffer(4 * 40 * 64), mc.DeviceBuffer(4 * 64 * 64)
+    with pytest.raises(mc.HipError):
+        mc.launch_matmul_cfg("double_buffered", da.ptr, db.ptr, dc.ptr, 64, 64, 40, None, 1, None, "mid")

@@ -257,6 +257,19 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
             byt = 4.0 * (m * k + k * n + m * n)
             e["gbs"] = byt / (ms * 1e-3) / 1e9
             e["frac_hbm"] = e["gbs"] / PEAK_HBM_GBS
+        if splits > 1 or m <= 32:
+            # The same product as a one-matmul graph compiled with autotune=1
+            # (split count and tile configuration timed at compile time).
+            g = mc.Compiled(f"graph gemm\ninput a : f32[{m}, {k}]\ninput b : f32[{k}, {n}]\nc = matmul a, b\n"
+                            f"output c\n", options={"autotune": 1})
+            g.upload([mc.uniform(m * k, 1, -1.0, 1.0), mc.uniform(k * n, 2, -1.0, 1.0)])
+            t = time_graph(mc, g, steps, warmup, warm_seconds=WARM_SECONDS)
+            tms = t["launch_ms"][0]
+            e["autotuned"] = {"ms": tms, "ms_range": t["launch_ms_range"][0], "kernel": g.matmul_kernels[0],
+                              "tflops": flop / (tms * 1e-3) / 1e12}
+            g.close()
+            log(f"gemm fp32 {m}x{n}x{k} autotuned ({e['autotuned']['kernel']}): {tms:.3f} ms "
+                f"{e['autotuned']['tflops']:.1f} TFLOP/s")
         out.append(e)
         log(f"gemm fp32 {m}x{n}x{k} {kernel}: {ms:.3f} ms {e['tflops']:.1f} TFLOP/s")
     return out

@@ -92,12 +92,18 @@ struct HipOptions {
     // legacy null stream). enqueue_launch and enqueue_with_events launch
     // directly.
     bool graph_replay = false;
-    // An Auto FP32 matmul's K split is chosen by timing the candidates on the
-    // device at compile time (double_buffered unsplit or split_k with 2, 4, ...
-    // splits) instead of by the split rule. Decisions are kept per device and
-    // shape for the process, and in MINICOMPILER_HIP_CACHE_DIR when set.
-    // Different split counts round differently (within the FP32 GEMM bound).
+    // An Auto FP32 matmul's K split and ring tile configuration are chosen by
+    // timing the candidates on the device at compile time (double_buffered
+    // unsplit or split_k with 2, 4, ... splits, on 128x128, 64x128 or 32x128
+    // tiles) instead of by the split rule and the planner. Decisions are kept
+    // per device and shape for the process, and in MINICOMPILER_HIP_CACHE_DIR
+    // when set. Different split counts round differently (within the FP32
+    // GEMM bound); the tile configuration does not change the bits.
     bool autotune = false;
+    // The FP32 ring tile configuration of double_buffered / split_k matmuls
+    // without autotune (MCHIP_RING_*: 0 the planner's own, 1 wide 128x128,
+    // 2 mid 64x128, 3 big 256x256, 4 thin 32x128). Same bits as the planner's.
+    int ring_config = 0;
 };
 
 // What the device reports (hipGetDeviceProperties / hipDeviceGetAttribute).

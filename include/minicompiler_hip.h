@@ -71,11 +71,13 @@ MC_API void mc_release(void* handle); /* capi.cpp:233-235 */
 
 /* mc_compile from graph text, with backend options
  * "matmul=NAME,vectorize=0|1,device=N,epilogue=0|1,tc_convert=0|1,graph=0|1,
- * autotune=0|1" (graph=1: mc_enqueue captures its launches into a HIP graph
- * once and replays it; rebinding buffers captures again. autotune=1: an
- * auto FP32 matmul's K split is chosen by timing the candidates on the
- * device at compile time, kept per shape for the process and in
- * MINICOMPILER_HIP_CACHE_DIR when set) and the elementwise
+ * autotune=0|1,ring=auto|wide|mid|big|thin" (graph=1: mc_enqueue captures its
+ * launches into a HIP graph once and replays it; rebinding buffers captures
+ * again. autotune=1: an auto FP32 matmul's K split and tile configuration
+ * are chosen by timing the candidates on the device at compile time, kept
+ * per shape for the process and in MINICOMPILER_HIP_CACHE_DIR when set.
+ * ring=: the FP32 ring tile configuration of double_buffered / split_k
+ * matmuls without autotune, same bits as the planner's) and the elementwise
  * kernel shape "ew_items=N,ew_nt_loads=0|1,ew_nt_stores=0|1,
  * ew_blocks_per_cu=N" (NULL or "" for defaults). */
 MC_API void* mc_compile_source(const char* text, const char* dims, const char* passes, const char* backend,

@@ -126,13 +126,21 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             o.graph_replay = value != "0" && value != "false";
         } else if (key == "autotune") {
             o.autotune = value != "0" && value != "false";
+        } else if (key == "ring") {
+            static const char* const names[] = {"auto", "wide", "mid", "big", "thin"};
+            int cfg = -1;
+            for (int i = 0; i < 5; ++i) {
+                if (value == names[i]) cfg = i;
+            }
+            if (cfg < 0) return Error{"option ring=" + value + ": expected auto, wide, mid, big or thin"};
+            o.ring_config = cfg;
         } else if (key == "ew_nt_loads") {
             o.nontemporal_loads = value != "0" && value != "false";
         } else if (key == "ew_nt_stores") {
             o.nontemporal_stores = value != "0" && value != "false";
         } else {
             return Error{"unknown option '" + key +
-                         "' (matmul, vectorize, device, epilogue, graph, autotune, tc_convert, ew_items, "
+                         "' (matmul, vectorize, device, epilogue, graph, autotune, ring, tc_convert, ew_items, "
                          "ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
         }
     }

@@ -493,6 +493,10 @@ private:
                          "): gfx950 has bf16 and fp16 matrix instructions but no xf32 (TF32) one"};
         }
         l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
+        if ((l->matmul == MatmulKernel::DoubleBuffered || l->matmul == MatmulKernel::SplitK) && l->k % 32 == 0 &&
+            l->n % 4 == 0) {
+            l->ring_cfg = options_.ring_config;  // a shape the ring cannot take keeps the planner's body
+        }
         if (options_.autotune && options_.matmul == MatmulKernel::Auto) {
             // The split count and ring configuration timed on this device
             // (double_buffered unsplit, split_k otherwise) instead of the

@@ -117,3 +117,23 @@ def test_a_forced_configuration_the_product_cannot_take_is_an_error(device, mc):
     da, db, dc = mc.DeviceBuffer(4 * 64 * 40), mc.DeviceBuffer(4 * 40 * 64), mc.DeviceBuffer(4 * 64 * 64)
     with pytest.raises(mc.HipError):
         mc.launch_matmul_cfg("double_buffered", da.ptr, db.ptr, dc.ptr, 64, 64, 40, None, 1, None, "mid")
+
+
+def test_the_ring_option_keeps_the_bits_of_the_planners_choice(device, mc, oracle):
+    # ring=wide|mid|thin on the MLP at B=1024 (GEMM1 split in two, GEMM2 in
+    # eight, each with its group fused into the store or the split sum): the
+    # same bits as the planner's configuration.
+    dims = {"B": 1024}
+    ref = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims)
+    inputs = uniform_inputs(oracle, ref.input_sizes, 3)
+    want = ref.run(inputs)
+    for ring in ("wide", "mid", "thin"):
+        print(f"case ring option {ring}", flush=True)
+        c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"ring": ring})
+        assert c.matmul_kernels == ref.matmul_kernels
+        got = c.run(inputs)
+        for p, q in zip(got, want):
+            assert np.array_equal(p.view(np.uint32), q.view(np.uint32)), ring
+        c.close()
+    with pytest.raises(mc.MinicompilerError):
+        mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"ring": "huge"})

@@ -545,6 +545,11 @@ def convert_f32(dtype: int, src: int, dst: int, count: int, stream=None) -> None
     _check(library().mc_convert_f32(dtype, src, dst, count, _stream_handle(stream)), "convert_f32")
 
 
+def sum_split_partials(partial: int, c: int, count: int, splits: int, stream=None) -> None:
+    """c[i] = partial[0][i] + ... + partial[splits-1][i], added in split order."""
+    _check(library().mc_sum_split_partials(partial, c, count, splits, _stream_handle(stream)), "sum_split_partials")
+
+
 def split_k_splits(m: int, n: int, k: int, cu_count: int, blocks_per_cu: int = 2) -> int:
     return library().mc_split_k_splits(m, n, k, cu_count, blocks_per_cu)
 

@@ -224,12 +224,29 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         os << "\tmc_gemm_f32_ring<" << cfg << ">(a, b, c, "
            << mnk << ", " << split << ", partial, epi);\n}\n\n";
     }
-    // Split K: the partial sums added in split order, then the epilogue.
+    // Split K: the partial sums added in split order (a left fold from split
+    // 0's value), then the epilogue. A lane issues `chunk` split loads before
+    // it adds any (indices past the last split clamped to it, their adds
+    // skipped), so they are in flight together.
+    const int chunk = constant ? std::max(1, std::min(fixed.depth - 1, 64)) : 16;
     os << "extern \"C\" __global__ void __launch_bounds__(256)\n" << kSumSplitsEpilogueKernelName
-       << "(const float* __restrict__ partial, float* __restrict__ c, unsigned count, int splits, McEpilogue epi)\n{\n"
+       << "(const float* __restrict__ partial, float* __restrict__ c, unsigned count, int splits_arg, "
+          "McEpilogue epi)\n{\n"
+       << (constant ? "\t(void)splits_arg;\n\tconst int splits = " + std::to_string(fixed.depth) + ";\n"
+                    : std::string("\tconst int splits = splits_arg;\n"))
        << "\tfor (unsigned i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {\n"
        << "\t\tfloat s = partial[i];\n"
-       << "\t\tfor (int z = 1; z < splits; ++z) s += partial[(unsigned long long)z * count + i];\n"
+       << "\t\tfor (int z0 = 1; z0 < splits; z0 += " << chunk << ") {\n"
+       << "\t\t\tfloat p[" << chunk << "];\n"
+       << "#pragma unroll\n"
+       << "\t\t\tfor (int j = 0; j < " << chunk << "; ++j) {\n"
+       << "\t\t\t\tconst int z = z0 + j < splits ? z0 + j : splits - 1;\n"
+       << "\t\t\t\tp[j] = partial[(unsigned long long)z * count + i];\n"
+       << "\t\t\t}\n"
+       << "#pragma unroll\n"
+       << "\t\t\tfor (int j = 0; j < " << chunk << "; ++j)\n"
+       << "\t\t\t\tif (z0 + j < splits) s += p[j];\n"
+       << "\t\t}\n"
        << "\t\tc[i] = epi(s, i);\n\t}\n}\n";
     return {os.str()};
 }

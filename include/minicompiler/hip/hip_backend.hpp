@@ -121,8 +121,12 @@ struct DeviceInfo {
     int runtime_version = 0;
     int driver_version = 0;
 
-    // Double data rate x memory clock x bus width.
-    double peak_bandwidth_gbs() const { return 2.0 * mem_clock_mhz * 1e6 * bus_width_bits / 8.0 / 1e9; }
+    // Transfers per reported memory clock x memory clock x bus width. The
+    // reference's formula counts two transfers (cuda_backend.hpp:73-76); the
+    // HIP runtime reports CDNA's HBM clock at a quarter of the per-pin data
+    // rate (MI355X: 2000 MHz for 8 Gb/s HBM3E on 8192 bits, 8.19 TB/s, the
+    // published 8 TB/s), so four here.
+    double peak_bandwidth_gbs() const { return 4.0 * mem_clock_mhz * 1e6 * bus_width_bits / 8.0 / 1e9; }
     // CDNA4 per CU and clock: 256 FP32 FLOP (matrix cores, or packed vector
     // FMA), 4096 dense bf16/fp16 FLOP on the matrix cores.
     double peak_fp32_gflops(double clock) const { return 256.0 * cu_count * clock * 1e6 / 1e9; }

@@ -49,6 +49,9 @@ def test_device_is_a_gfx950(device, mc):
     assert device["arch"].startswith("gfx950"), device["arch"]
     assert device["cu_count"] > 0 and device["wave_size"] == 64
     assert device["peak_bandwidth_gbs"] > 0 and device["peak_fp32_gflops"] > 0
+    # HBM3E on gfx950 (MI350X / MI355X): 8 TB/s published; the runtime's
+    # memory clock and bus width give 8.19 TB/s at four transfers per clock.
+    assert 7000 < device["peak_bandwidth_gbs"] < 9000, device["peak_bandwidth_gbs"]
     assert "hip" in mc.Compiled(unary_graph("neg", (4,)), backend="hip").backend
 
 

@@ -171,6 +171,21 @@ MC_API int mc_launch_matmul(int kernel, const float* a, const float* b, float* c
  * 32, N not of 4, operands not 16-byte aligned) or for other kernels. */
 MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
                                 void* stream, int splits, float* workspace, int ring_cfg);
+/* mc_launch_matmul without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference, whose
+ * callers pass the workspace (launch_matmul, matmul_kernels.hpp:45-52). The
+ * split-K partials go to a per-GPU scratch array of mc_noalloc_scratch_bytes()
+ * (32 MiB) inside the library, held until the process ends; nothing is
+ * allocated per call. A product whose partials (splits x m x n floats for
+ * split_k and the tensor-core kernels with splits > 1) exceed it is refused
+ * with hipErrorInvalidValue (1) and a message in mc_last_error(). Every call
+ * on one GPU shares its array: calls whose executions overlap on one GPU
+ * (other streams, other threads) race; calls ordered on one stream do not.
+ * Same kernels and bits as mc_launch_matmul with the same `splits`. */
+MC_API int mc_launch_matmul_noalloc(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                    void* stream, int splits);
+MC_API unsigned long long mc_noalloc_scratch_bytes(void);
 /* The matrix-core kernels on inputs already stored as bf16 (dtype 1) or fp16
  * (dtype 2); fp32 accumulation and output. */
 MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,

@@ -100,6 +100,8 @@ _SIGNATURES = {
     "mc_launch_matmul": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "mc_launch_matmul_cfg": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _i]),
     "mc_launch_matmul_lowp": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "mc_launch_matmul_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i]),
+    "mc_noalloc_scratch_bytes": (_c.c_ulonglong, []),
     "mc_convert_f32": (_i, [_i, _vp, _vp, _sz, _vp]),
     "mc_sum_split_partials": (_i, [_vp, _vp, _sz, _i, _vp]),
     "mc_split_k_splits": (_i, [_i, _i, _i, _i, _i]),
@@ -520,6 +522,21 @@ def launch_matmul(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: 
     kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
     _check(library().mc_launch_matmul(kid, a, b, c, m, n, k, _stream_handle(stream), splits, workspace),
            f"launch_matmul({matmul_kernel_name(kid)})")
+
+
+def launch_matmul_noalloc(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: int, stream=None,
+                          splits: int = 1) -> None:
+    """launch_matmul with the split-K partials in the library's per-GPU
+    scratch array (noalloc_scratch_bytes()); allocates nothing. Calls that
+    overlap on one GPU race on the array."""
+    kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
+    rc = library().mc_launch_matmul_noalloc(kid, a, b, c, m, n, k, _stream_handle(stream), splits)
+    if rc != 0:
+        raise HipError(f"launch_matmul_noalloc({matmul_kernel_name(kid)}): {last_error()}", rc)
+
+
+def noalloc_scratch_bytes() -> int:
+    return int(library().mc_noalloc_scratch_bytes())
 
 
 RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4}

@@ -738,6 +738,23 @@ MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, floa
     return mchip_launch_matmul_cfg(kernel, a, b, c, m, n, k, stream, splits, workspace, ring_cfg);
 }
 
+MC_API int mc_launch_matmul_noalloc(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                    void* stream, int splits) {
+    const unsigned long long need = mchip_noalloc_required_bytes(kernel, m, n, splits);
+    const unsigned long long have = mchip_noalloc_scratch_bytes();
+    if (need > have) {
+        g_last_error = "mc_launch_matmul_noalloc: " + std::to_string(splits) + " splits of a " + std::to_string(m) +
+                       "x" + std::to_string(n) + " product need " + std::to_string(need) +
+                       " bytes of partials, more than the library's " + std::to_string(have) + "-byte scratch";
+        return 1;  // hipErrorInvalidValue
+    }
+    const int rc = mchip_launch_matmul_noalloc(kernel, a, b, c, m, n, k, stream, splits);
+    if (rc != 0) g_last_error = std::string("mc_launch_matmul_noalloc: ") + mchip_error_string(rc);
+    return rc;
+}
+
+MC_API unsigned long long mc_noalloc_scratch_bytes(void) { return mchip_noalloc_scratch_bytes(); }
+
 MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,
                                  void* stream, int splits, float* workspace) {
     return mchip_launch_matmul_lowp(kernel, dtype, a, b, c, m, n, k, stream, splits, workspace);

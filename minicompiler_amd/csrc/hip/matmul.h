@@ -69,6 +69,16 @@ int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cf
 int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
                             int splits, float* workspace, int ring_cfg);
 
+/* mchip_launch_matmul with the split-K partials in the library's per-device
+ * scratch array (matmul_noalloc.hip) instead of a caller workspace; no
+ * device memory is allocated. hipErrorInvalidValue when the partials
+ * (mchip_noalloc_required_bytes) exceed mchip_noalloc_scratch_bytes().
+ * Calls that overlap on one GPU race on the array. */
+int mchip_launch_matmul_noalloc(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                void* stream, int splits);
+unsigned long long mchip_noalloc_scratch_bytes(void);
+unsigned long long mchip_noalloc_required_bytes(int kernel, int m, int n, int splits);
+
 /* Elementwise fp32 -> bf16/fp16 (round to nearest even), for staging. */
 int mchip_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream);
 

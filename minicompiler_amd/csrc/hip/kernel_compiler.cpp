@@ -2,12 +2,18 @@
 
 #include "hip_rt.h"
 
+#include <fcntl.h>
+#include <unistd.h>
+
+#include <atomic>
+#include <cerrno>
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <fstream>
 #include <sstream>
+#include <thread>
 
 namespace minicompiler::hip {
 
@@ -39,15 +45,26 @@ bool read_file(const std::string& path, std::string* out) {
     return !out->empty();
 }
 
-// A cache file: the magic line, the key's length in decimal and a newline,
-// the key itself, then the code object. A file whose key differs from the
-// requested one (a hash collision, or a key from another compiler) is not
-// used.
-constexpr const char* kCacheMagic = "minicompiler-hip code object v1\n";
+// A cache file: the magic line; the key's length in decimal and a newline;
+// the key itself; the code object's length in decimal, a space, its FNV-1a
+// hash in hex and a newline; then the code object. A file whose key differs
+// from the requested one (a hash collision, or a key from another compiler)
+// or whose code does not have the recorded length and hash (a torn or
+// truncated write) is a miss: the kernel is compiled again.
+constexpr const char* kCacheMagic = "minicompiler-hip code object v2\n";
+
+std::string hex64(std::uint64_t v) {
+    char buf[17];
+    std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(v));
+    return buf;
+}
 
 std::string cache_file_contents(const std::string& key, const std::string& code) {
-    return std::string(kCacheMagic) + std::to_string(key.size()) + '\n' + key + code;
+    return std::string(kCacheMagic) + std::to_string(key.size()) + '\n' + key + std::to_string(code.size()) + ' ' +
+           hex64(fnv1a64(code)) + '\n' + code;
 }
+
+bool all_digits(const std::string& s) { return !s.empty() && s.find_first_not_of("0123456789") == std::string::npos; }
 
 bool code_from_cache_file(const std::string& file, const std::string& key, std::string* code) {
     const std::string magic(kCacheMagic);
@@ -55,21 +72,43 @@ bool code_from_cache_file(const std::string& file, const std::string& key, std::
     const std::size_t nl = file.find('\n', magic.size());
     if (nl == std::string::npos) return false;
     const std::string len_text = file.substr(magic.size(), nl - magic.size());
-    if (len_text.empty() || len_text.find_first_not_of("0123456789") != std::string::npos) return false;
+    if (!all_digits(len_text) || len_text.size() > 18) return false;
     const std::size_t len = std::stoull(len_text);
     if (len != key.size() || file.size() <= nl + 1 + len || file.compare(nl + 1, len, key) != 0) return false;
-    *code = file.substr(nl + 1 + len);
+    const std::size_t head = nl + 1 + len;
+    const std::size_t nl2 = file.find('\n', head);
+    const std::size_t sp = file.find(' ', head);
+    if (nl2 == std::string::npos || sp == std::string::npos || sp > nl2) return false;
+    const std::string code_len = file.substr(head, sp - head);
+    if (!all_digits(code_len) || code_len.size() > 18) return false;
+    const std::size_t clen = std::stoull(code_len);
+    if (file.size() - (nl2 + 1) != clen || clen == 0) return false;
+    std::string body = file.substr(nl2 + 1);
+    if (file.compare(sp + 1, nl2 - sp - 1, hex64(fnv1a64(body))) != 0) return false;
+    *code = std::move(body);
     return true;
 }
 
+// Writes `data` to a temporary file of a name no other writer uses (this
+// process's id, a per-process counter and the thread's id, created with
+// O_EXCL), then renames it over `path`: readers see the old file or the
+// whole new one. Any failure leaves `path` alone.
 void write_file_atomically(const std::string& path, const std::string& data) {
-    const std::string tmp = path + ".tmp" + std::to_string(reinterpret_cast<std::uintptr_t>(&data));
-    {
-        std::ofstream f(tmp, std::ios::binary);
-        if (!f) return;
-        f.write(data.data(), static_cast<std::streamsize>(data.size()));
+    static std::atomic<unsigned long long> counter{0};
+    const std::string tmp = path + ".tmp." + std::to_string(static_cast<long long>(getpid())) + '.' +
+                            std::to_string(counter.fetch_add(1)) + '.' +
+                            hex64(std::hash<std::thread::id>{}(std::this_thread::get_id()));
+    const int fd = open(tmp.c_str(), O_WRONLY | O_CREAT | O_EXCL | O_CLOEXEC, 0644);
+    if (fd < 0) return;
+    std::size_t done = 0;
+    while (done < data.size()) {
+        const ssize_t w = write(fd, data.data() + done, data.size() - done);
+        if (w < 0 && errno == EINTR) continue;
+        if (w <= 0) break;
+        done += static_cast<std::size_t>(w);
     }
-    std::rename(tmp.c_str(), path.c_str());
+    const bool ok = close(fd) == 0 && done == data.size();
+    if (!ok || std::rename(tmp.c_str(), path.c_str()) != 0) unlink(tmp.c_str());
 }
 
 std::string cache_key(const std::string& arch, const std::string& source) {

@@ -230,7 +230,11 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     const bool vec = n % 4 == 0 && k % 4 == 0 && aligned16(a) && aligned16(b);
     float* out_ws = depth > 1 ? workspace : nullptr;
     unsigned ring_grid = 0, ring_block = 0;
-    const int ring = double_buffer && vec && aligned16(c)
+    // The ring body stores C (or a split's partial) 4, 8 or 16 bytes at a
+    // time: the destination must be 16-byte aligned, as the reference
+    // requires of the workspace (matmul_kernels.cu:324).
+    const bool dest_aligned = depth > 1 ? aligned16(workspace) : aligned16(c);
+    const int ring = double_buffer && vec && dest_aligned
                          ? mchip_f32_ring_plan_cfg(m, n, k, depth, device_cu_count(), ring_cfg, &ring_grid, &ring_block)
                          : MCHIP_RING_NONE;
     if (ring_cfg != MCHIP_RING_NONE && ring != ring_cfg) return hipErrorInvalidValue;

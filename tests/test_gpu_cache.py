@@ -54,3 +54,21 @@ def test_second_process_loads_kernels_from_disk_and_rejects_a_foreign_key(device
     third = run_child(tmp_path)
     assert third["jit_ms"] > 0
     assert (third["sum"], third["bits"]) == (first["sum"], first["bits"])
+    assert not list(tmp_path.glob("*.tmp*")), "a temporary file was left behind"
+
+
+def test_a_truncated_code_object_is_a_miss_and_is_compiled_again(device, tmp_path):
+    # Each file records its code object's length and hash: a torn or cut-off
+    # write is recompiled (and the file rewritten), not loaded.
+    first = run_child(tmp_path)
+    files = sorted(tmp_path.glob("mc_*.co"))
+    assert files
+    for f in files:
+        data = f.read_bytes()
+        f.write_bytes(data[:-100])
+    second = run_child(tmp_path)
+    assert second["jit_ms"] > 0
+    assert (second["sum"], second["bits"]) == (first["sum"], first["bits"])
+    third = run_child(tmp_path)
+    assert third["jit_ms"] == 0.0, "the rewritten files load again"
+    assert not list(tmp_path.glob("*.tmp*"))

@@ -137,3 +137,26 @@ def test_the_ring_option_keeps_the_bits_of_the_planners_choice(device, mc, oracl
         c.close()
     with pytest.raises(mc.MinicompilerError):
         mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"ring": "huge"})
+
+
+@pytest.mark.parametrize("m,k,n,splits", [(256, 2048, 256, 8), (16, 4096, 1024, 4)])
+def test_split_k_with_a_workspace_off_16_bytes_gives_the_aligned_bits(device, mc, oracle, m, k, n, splits):
+    # The ring body writes partials 4-16 bytes at a time, so a workspace that
+    # is not 16-byte aligned (a C-ABI caller may pass one) must send the
+    # product to the two-stage body, whose scalar stores give the same bits.
+    print(f"case split_k unaligned workspace {m}x{k}x{n} splits={splits}", flush=True)
+    a = oracle.uniform(m * k, 21, -1.0, 1.0)
+    b = oracle.uniform(k * n, 22, -1.0, 1.0)
+    da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
+    ws_bytes = mc.matmul_workspace_bytes("split_k", m, n, splits)
+    ws = mc.DeviceBuffer(ws_bytes + 64)
+    outs = []
+    for offset in (0, 4, 8):
+        dc = mc.DeviceBuffer.from_array(np.full(m * n, np.nan, dtype=np.float32))
+        mc.launch_matmul("split_k", da.ptr, db.ptr, dc.ptr, m, n, k, None, splits, ws.ptr + offset)
+        mc.synchronize()
+        outs.append(dc.download())
+    for o in outs[1:]:
+        assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))
+    exact, absdot = oracle.gemm_f64(a, b, m, k, n)
+    assert np.all(np.abs(outs[0].astype(np.float64) - exact) <= fp32_gemm_bound(exact, absdot, k))

@@ -68,8 +68,14 @@ public:
     Status verify() const;
 
 private:
-    Status check_operands(const std::vector<NodeId>& inputs) const;
-    NodeId append(Node node);
+    // Whether `n` may stand at index `position` of this graph: operands
+    // earlier than it, the op's arity, a storable type, a payload or program
+    // that fits it, and for primitive ops the type the op infers. Both the
+    // add_* calls and verify() go through it.
+    Status vet(const Node& n, std::size_t position) const;
+    // vet(n) at the end of the graph, then store it (an unnamed node becomes
+    // "<op>_<id>"; an input also joins the input list).
+    Result<NodeId> admit(Node n);
 
     std::string name_;
     std::vector<Node> nodes_;

@@ -41,8 +41,6 @@ public:
     const Graph& graph() const { return graph_; }
 
 private:
-    NodeId keep(Result<NodeId> r);
-
     Graph graph_;
     std::optional<Error> first_error_;
 };

@@ -1,42 +1,56 @@
-// Sticky-error builder (reference: src/graph_builder.cpp:5-54).
+// The graph builder with a sticky error (the contract of the reference's
+// src/graph_builder.cpp): once a call fails, every later call is a no-op
+// returning kNoNode, and build() reports the first failure.
 
 #include "minicompiler/graph_builder.hpp"
 
 namespace minicompiler {
 
-NodeId GraphBuilder::keep(Result<NodeId> r) {
-    if (r.ok()) return r.value();
-    first_error_ = r.error();
-    return kNoNode;
+namespace {
+
+// Runs `add` unless an earlier call failed; a failure is remembered.
+template <typename Add>
+NodeId guarded(std::optional<Error>& first_error, Add&& add) {
+    if (first_error) return kNoNode;
+    Result<NodeId> r = add();
+    if (!r.ok()) {
+        first_error = r.error();
+        return kNoNode;
+    }
+    return r.value();
 }
 
+}  // namespace
+
 NodeId GraphBuilder::input(std::string name, Shape shape) {
-    if (first_error_) return kNoNode;
-    return keep(graph_.add_input(std::move(name), TensorType(std::move(shape))));
+    return guarded(first_error_, [&] { return graph_.add_input(std::move(name), TensorType(std::move(shape))); });
 }
 
 NodeId GraphBuilder::constant(std::string name, Shape shape, std::vector<float> values) {
-    if (first_error_) return kNoNode;
-    return keep(graph_.add_constant(std::move(name), TensorType(std::move(shape)), std::move(values)));
+    return guarded(first_error_, [&] {
+        return graph_.add_constant(std::move(name), TensorType(std::move(shape)), std::move(values));
+    });
 }
 
-NodeId GraphBuilder::scalar(std::string name, float value) { return constant(std::move(name), Shape{}, {value}); }
+NodeId GraphBuilder::scalar(std::string name, float value) {
+    return constant(std::move(name), Shape{}, std::vector<float>{value});
+}
 
 NodeId GraphBuilder::op(OpKind kind, std::vector<NodeId> inputs, std::string name) {
-    if (first_error_) return kNoNode;
-    return keep(graph_.add_op(kind, std::move(inputs), std::move(name)));
+    return guarded(first_error_, [&] { return graph_.add_op(kind, std::move(inputs), std::move(name)); });
 }
 
 void GraphBuilder::output(NodeId id) {
-    if (first_error_) return;
-    Status st = graph_.add_output(id);
-    if (!st.ok()) first_error_ = st.error();
+    guarded(first_error_, [&]() -> Result<NodeId> {
+        Status st = graph_.add_output(id);
+        if (!st.ok()) return st.error();
+        return id;
+    });
 }
 
 Result<Graph> GraphBuilder::build() && {
     if (first_error_) return *first_error_;
-    Status st = graph_.verify();
-    if (!st.ok()) return st.error();
+    if (Status st = graph_.verify(); !st.ok()) return st.error();
     return std::move(graph_);
 }
 

@@ -1,13 +1,24 @@
-// Lifetime-based buffer planner (reference: src/runtime/memory_plan.cpp:12-70).
-// The assignment rule is the reference's, step for step, because buffer
-// counts and reuse are part of the compiled contract (tests pin them):
-// best fit among free buffers, else grow the largest free buffer, else open
-// a new one; a node's operands are released only after its own buffer is
-// chosen; an unread value releases its buffer at once.
+// Lifetime-based buffer planning (the contract of the reference's
+// src/runtime/memory_plan.cpp: its buffer counts and sizes are pinned by the
+// reference's tests).
+//
+// Node ids are time steps. Each pooled value lives from its own step to its
+// last reader's (outputs to the end of the run; an unread value only for its
+// own step). The planner walks the steps keeping the free buffers in a pool
+// ordered by size:
+//   1. the step's value takes the smallest free buffer that holds it; if none
+//      does, the largest free buffer, grown to its size; if the pool is
+//      empty, a new buffer;
+//   2. then the values whose lifetime ends at this step return their buffers
+//      to the pool (so a node never writes a buffer it still reads), and so
+//      does the step's own value when nothing reads it.
+// Among free buffers of one size the one returned first is taken first. The
+// counts and sizes do not depend on that choice: buffers of one size are
+// interchangeable for every later step.
 
 #include "minicompiler/runtime/memory_plan.hpp"
 
-#include <algorithm>
+#include <map>
 #include <numeric>
 
 namespace minicompiler {
@@ -17,59 +28,59 @@ std::size_t MemoryPlan::bytes_with_reuse() const {
 }
 
 MemoryPlan plan_memory(const Graph& graph, const PlanOptions& options) {
-    const std::size_t n = graph.num_nodes();
+    const std::size_t steps = graph.num_nodes();
     MemoryPlan plan;
-    plan.buffer_of.assign(n, MemoryPlan::kNotPooled);
-    plan.last_use.assign(n, kNoNode);
-    for (std::size_t i = 0; i < n; ++i) {
-        for (NodeId in : graph.node(static_cast<NodeId>(i)).inputs) {
-            plan.last_use[static_cast<std::size_t>(in)] = static_cast<NodeId>(i);
+    plan.buffer_of.assign(steps, MemoryPlan::kNotPooled);
+    plan.last_use.assign(steps, kNoNode);
+    for (std::size_t t = 0; t < steps; ++t) {
+        for (NodeId in : graph.node(static_cast<NodeId>(t)).inputs) {
+            plan.last_use[static_cast<std::size_t>(in)] = static_cast<NodeId>(t);
         }
     }
-    for (NodeId out : graph.outputs()) plan.last_use[static_cast<std::size_t>(out)] = static_cast<NodeId>(n);
+    for (NodeId out : graph.outputs()) plan.last_use[static_cast<std::size_t>(out)] = static_cast<NodeId>(steps);
 
-    std::vector<std::int32_t> free_list;
-    for (std::size_t i = 0; i < n; ++i) {
-        const auto id = static_cast<NodeId>(i);
-        const Node& node = graph.node(id);
-        if (!is_compute(node.op)) continue;
-        const bool pooled = options.pool_outputs || !graph.is_output(id);
-        if (pooled) {
-            const std::size_t need = node.type.size_bytes();
-            plan.bytes_without_reuse += need;
-            auto pick = free_list.end();
-            for (auto it = free_list.begin(); it != free_list.end(); ++it) {
-                const std::size_t have = plan.buffer_bytes[static_cast<std::size_t>(*it)];
-                if (have >= need && (pick == free_list.end() || have < plan.buffer_bytes[static_cast<std::size_t>(*pick)])) {
-                    pick = it;
-                }
-            }
-            if (pick == free_list.end() && !free_list.empty()) {
-                pick = std::max_element(free_list.begin(), free_list.end(), [&](std::int32_t a, std::int32_t b) {
-                    return plan.buffer_bytes[static_cast<std::size_t>(a)] < plan.buffer_bytes[static_cast<std::size_t>(b)];
-                });
-                plan.buffer_bytes[static_cast<std::size_t>(*pick)] = need;
-            }
-            if (pick != free_list.end()) {
-                plan.buffer_of[i] = *pick;
-                free_list.erase(pick);
-            } else {
-                plan.buffer_of[i] = static_cast<std::int32_t>(plan.buffer_bytes.size());
-                plan.buffer_bytes.push_back(need);
-            }
+    auto pooled = [&](std::size_t v) {
+        const NodeId id = static_cast<NodeId>(v);
+        return is_compute(graph.node(id).op) && (options.pool_outputs || !graph.is_output(id));
+    };
+    // ends_at[t]: pooled values whose last reader is step t, in id order.
+    std::vector<std::vector<std::size_t>> ends_at(steps);
+    for (std::size_t v = 0; v < steps; ++v) {
+        const NodeId last = plan.last_use[v];
+        if (pooled(v) && last != kNoNode && static_cast<std::size_t>(last) < steps) {
+            ends_at[static_cast<std::size_t>(last)].push_back(v);
         }
-        // Release operands whose last reader is this node (once per distinct
-        // operand), also when this node's own value is not pooled.
-        for (std::size_t k = 0; k < node.inputs.size(); ++k) {
-            const NodeId in = node.inputs[k];
-            const bool seen = std::find(node.inputs.begin(), node.inputs.begin() + static_cast<std::ptrdiff_t>(k), in) !=
-                              node.inputs.begin() + static_cast<std::ptrdiff_t>(k);
-            const auto ii = static_cast<std::size_t>(in);
-            if (!seen && plan.buffer_of[ii] != MemoryPlan::kNotPooled && plan.last_use[ii] == id) {
-                free_list.push_back(plan.buffer_of[ii]);
-            }
+    }
+
+    std::multimap<std::size_t, std::int32_t> pool;  // free buffers by size, in the order returned
+    auto give_back = [&](std::int32_t buffer) {
+        pool.emplace(plan.buffer_bytes[static_cast<std::size_t>(buffer)], buffer);
+    };
+    auto take = [&](std::size_t bytes) -> std::int32_t {
+        auto fit = pool.lower_bound(bytes);
+        if (fit == pool.end() && !pool.empty()) {
+            fit = pool.lower_bound(pool.rbegin()->first);  // the first returned of the largest
+            plan.buffer_bytes[static_cast<std::size_t>(fit->second)] = bytes;
         }
-        if (pooled && plan.last_use[i] == kNoNode) free_list.push_back(plan.buffer_of[i]);
+        if (fit == pool.end()) {
+            plan.buffer_bytes.push_back(bytes);
+            return static_cast<std::int32_t>(plan.buffer_bytes.size() - 1);
+        }
+        const std::int32_t buffer = fit->second;
+        pool.erase(fit);
+        return buffer;
+    };
+
+    for (std::size_t t = 0; t < steps; ++t) {
+        if (!is_compute(graph.node(static_cast<NodeId>(t)).op)) continue;
+        const bool own = pooled(t);
+        if (own) {
+            const std::size_t bytes = graph.node(static_cast<NodeId>(t)).type.size_bytes();
+            plan.bytes_without_reuse += bytes;
+            plan.buffer_of[t] = take(bytes);
+        }
+        for (std::size_t v : ends_at[t]) give_back(plan.buffer_of[v]);
+        if (own && plan.last_use[t] == kNoNode) give_back(plan.buffer_of[t]);
     }
     return plan;
 }

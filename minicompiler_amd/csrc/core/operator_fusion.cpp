@@ -1,145 +1,155 @@
-// Elementwise fusion (reference: src/passes/operator_fusion.cpp:10-144).
-// Group growth and instruction order follow the reference exactly, since
-// stage counts and programs are part of the compiled contract: roots are
-// visited from the highest id down, candidate producers are taken highest id
-// first, members are emitted in ascending id order, and within a member the
-// first operand's load or immediate is emitted before the second's.
+// Elementwise fusion (the contract of the reference's
+// src/passes/operator_fusion.cpp: which nodes share a kernel and the order of
+// the instructions in each program are pinned by the reference's known
+// answers, e.g. the GELU chain's one load and four immediates).
+//
+// Groups. Roots are taken from the highest unassigned elementwise id down.
+// From a root the group grows toward its producers: the ids below it are
+// swept downward, and an id the group reads (a candidate) joins when it is
+// an unassigned elementwise node of the root's shape, not a graph output,
+// whose every reader is already in the group. Its operands become
+// candidates. A node's readers all have higher ids, so the downward sweep
+// decides every reader before the node itself: the group is closed under
+// "all readers inside", and no value it computes leaves the kernel.
+//
+// Programs. Members are emitted in ascending id order. A member's operands
+// get registers the first time they are read, operand a before operand b: a
+// member computed earlier in the group is its register, a one-element
+// constant becomes an immediate, anything else a load of the next external
+// input.
 
 #include "minicompiler/passes/operator_fusion.hpp"
 
 #include <algorithm>
-#include <map>
 #include <memory>
-#include <queue>
 
 namespace minicompiler {
 
 std::vector<std::vector<NodeId>> find_fusion_groups(const Graph& graph) {
     const std::size_t n = graph.num_nodes();
-    const auto users = graph.compute_users();
-    std::vector<int> group(n, -1);
-    std::vector<std::vector<NodeId>> found;
+    const std::vector<std::vector<NodeId>> readers = graph.compute_users();
+    std::vector<int> group_of(n, -1);
+    std::vector<char> wanted(n, 0);  // read by the group being grown
+    std::vector<std::vector<NodeId>> by_root;  // highest root first
 
-    for (std::size_t i = n; i-- > 0;) {
-        const Node& root = graph.node(static_cast<NodeId>(i));
-        if (!is_elementwise(root.op) || group[i] >= 0) continue;
-        const int g = static_cast<int>(found.size());
-        group[i] = g;
-        std::vector<NodeId> members{static_cast<NodeId>(i)};
-        std::priority_queue<NodeId> frontier;
-        for (NodeId in : root.inputs) frontier.push(in);
-        while (!frontier.empty()) {
-            const NodeId p = frontier.top();
-            frontier.pop();
-            const auto pi = static_cast<std::size_t>(p);
-            if (group[pi] >= 0) continue;
-            const Node& pn = graph.node(p);
-            if (!is_elementwise(pn.op) || pn.type.shape != root.type.shape || graph.is_output(p)) continue;
-            // Every reader of p must already be inside: p's value never
-            // leaves the kernel, and the group stays convex.
-            const bool contained =
-                std::all_of(users[pi].begin(), users[pi].end(), [&](NodeId u) { return group[u] == g; });
-            if (!contained) continue;
-            group[pi] = g;
-            members.push_back(p);
-            for (NodeId in : pn.inputs) frontier.push(in);
+    for (std::size_t r = n; r-- > 0;) {
+        const Node& root = graph.node(static_cast<NodeId>(r));
+        if (!is_elementwise(root.op) || group_of[r] >= 0) continue;
+        const int g = static_cast<int>(by_root.size());
+        group_of[r] = g;
+        std::vector<NodeId> members{static_cast<NodeId>(r)};
+        std::size_t lowest = r;  // no candidate lies below it
+        auto want_operands = [&](const Node& m) {
+            for (NodeId in : m.inputs) {
+                wanted[static_cast<std::size_t>(in)] = 1;
+                lowest = std::min(lowest, static_cast<std::size_t>(in));
+            }
+        };
+        want_operands(root);
+        for (std::size_t p = r; p-- > lowest;) {
+            if (!wanted[p]) continue;
+            wanted[p] = 0;
+            const Node& pn = graph.node(static_cast<NodeId>(p));
+            if (group_of[p] >= 0 || !is_elementwise(pn.op) || pn.type.shape != root.type.shape ||
+                graph.is_output(static_cast<NodeId>(p))) {
+                continue;
+            }
+            bool enclosed = true;
+            for (NodeId u : readers[p]) enclosed = enclosed && group_of[static_cast<std::size_t>(u)] == g;
+            if (!enclosed) continue;
+            group_of[p] = g;
+            members.push_back(static_cast<NodeId>(p));
+            want_operands(pn);
         }
-        std::sort(members.begin(), members.end());
-        found.push_back(std::move(members));
+        // Every mark lay in [lowest, r) and the sweep cleared it on its way down.
+        std::vector<NodeId> ascending(members.rbegin(), members.rend());
+        by_root.push_back(std::move(ascending));
     }
 
-    // Roots were visited last-first; report them first-last.
-    std::vector<std::vector<NodeId>> groups;
-    for (auto it = found.rbegin(); it != found.rend(); ++it) {
-        if (it->size() >= 2) groups.push_back(std::move(*it));
+    std::vector<std::vector<NodeId>> groups;  // lowest root first, singletons dropped
+    for (std::size_t i = by_root.size(); i-- > 0;) {
+        if (by_root[i].size() >= 2) groups.push_back(std::move(by_root[i]));
     }
     return groups;
 }
 
 namespace {
 
-// Builds one group's FusedProgram over its external operands.
-class ProgramEmitter {
-public:
-    ProgramEmitter(const Graph& graph, const std::vector<NodeId>& new_id) : graph_(graph), new_id_(new_id) {}
-
-    void member(NodeId id) {
-        const Node& node = graph_.node(id);
-        const std::int32_t x = reg(node.inputs[0]);
-        if (is_unary_elementwise(node.op)) {
-            push(id, FusedInstr::unary(node.op, x));
-        } else {
-            const std::int32_t y = reg(node.inputs[1]);
-            push(id, FusedInstr::binary(node.op, x, y));
-        }
-        program_->source_nodes.push_back(node.name);
-    }
-
-    std::shared_ptr<FusedProgram> program() const { return program_; }
-    const std::vector<NodeId>& externals() const { return externals_; }
-
-private:
-    // The register holding node `id`, created on first use for an external
-    // operand: an immediate for a one-element constant, else a load.
-    std::int32_t reg(NodeId id) {
-        const auto it = reg_.find(id);
-        if (it != reg_.end()) return it->second;
-        const Node& node = graph_.node(id);
-        if (node.op == OpKind::Constant && node.type.num_elements() == 1) {
-            return push(id, FusedInstr::imm((*node.constant)[0]));
-        }
-        externals_.push_back(new_id_[static_cast<std::size_t>(id)]);
-        return push(id, FusedInstr::load(static_cast<std::int32_t>(externals_.size()) - 1));
-    }
-
-    std::int32_t push(NodeId id, FusedInstr ins) {
-        program_->instrs.push_back(ins);
-        const auto r = static_cast<std::int32_t>(program_->instrs.size()) - 1;
-        reg_[id] = r;
-        return r;
-    }
-
-    const Graph& graph_;
-    const std::vector<NodeId>& new_id_;
-    std::shared_ptr<FusedProgram> program_ = std::make_shared<FusedProgram>();
-    std::vector<NodeId> externals_;
-    std::map<NodeId, std::int32_t> reg_;
+struct EmittedGroup {
+    std::shared_ptr<FusedProgram> program = std::make_shared<FusedProgram>();
+    std::vector<NodeId> externals;  // operand ids in the new graph, in load order
 };
+
+// The FusedProgram of one group (members ascending). `new_id` maps old ids
+// of already rebuilt nodes to the new graph's.
+EmittedGroup emit_group(const Graph& graph, const std::vector<NodeId>& members, const std::vector<NodeId>& new_id) {
+    EmittedGroup out;
+    std::vector<std::pair<NodeId, std::int32_t>> regs;  // node -> register, in emission order
+    auto append = [&](NodeId id, const FusedInstr& ins) {
+        out.program->instrs.push_back(ins);
+        const auto r = static_cast<std::int32_t>(out.program->instrs.size() - 1);
+        regs.emplace_back(id, r);
+        return r;
+    };
+    auto operand = [&](NodeId id) -> std::int32_t {
+        for (const auto& [node, r] : regs) {
+            if (node == id) return r;
+        }
+        const Node& src = graph.node(id);
+        if (src.op == OpKind::Constant && src.type.num_elements() == 1) {
+            return append(id, FusedInstr::imm((*src.constant)[0]));
+        }
+        out.externals.push_back(new_id[static_cast<std::size_t>(id)]);
+        return append(id, FusedInstr::load(static_cast<std::int32_t>(out.externals.size() - 1)));
+    };
+    for (NodeId m : members) {
+        const Node& node = graph.node(m);
+        const std::int32_t a = operand(node.inputs[0]);
+        if (is_binary_elementwise(node.op)) {
+            const std::int32_t b = operand(node.inputs[1]);
+            append(m, FusedInstr::binary(node.op, a, b));
+        } else {
+            append(m, FusedInstr::unary(node.op, a));
+        }
+        out.program->source_nodes.push_back(node.name);
+    }
+    return out;
+}
 
 }  // namespace
 
 Result<Graph> fuse_elementwise(const Graph& graph, PassReport* report) {
-    const auto groups = find_fusion_groups(graph);
-    std::vector<int> group_of(graph.num_nodes(), -1);
+    const std::vector<std::vector<NodeId>> groups = find_fusion_groups(graph);
+    // root_of[v]: the group whose last (root) member is v; member[v]: v is in a group.
+    std::vector<int> root_of(graph.num_nodes(), -1);
+    std::vector<char> member(graph.num_nodes(), 0);
+    std::size_t fused_ops = 0;
     for (std::size_t g = 0; g < groups.size(); ++g) {
-        for (NodeId m : groups[g]) group_of[static_cast<std::size_t>(m)] = static_cast<int>(g);
+        for (NodeId m : groups[g]) member[static_cast<std::size_t>(m)] = 1;
+        root_of[static_cast<std::size_t>(groups[g].back())] = static_cast<int>(g);
+        fused_ops += groups[g].size();
     }
 
     Graph result(graph.name());
     std::vector<NodeId> new_id(graph.num_nodes(), kNoNode);
-    std::size_t fused_ops = 0;
     for (std::size_t i = 0; i < graph.num_nodes(); ++i) {
         const Node& node = graph.node(static_cast<NodeId>(i));
-        if (group_of[i] < 0) {
+        Result<NodeId> id = kNoNode;
+        if (root_of[i] >= 0) {
+            EmittedGroup e = emit_group(graph, groups[static_cast<std::size_t>(root_of[i])], new_id);
+            id = result.add_fused(std::move(e.externals), std::move(e.program), node.type, node.name);
+        } else if (!member[i]) {
             std::vector<NodeId> operands;
             for (NodeId in : node.inputs) operands.push_back(new_id[static_cast<std::size_t>(in)]);
-            Result<NodeId> id = result.copy_node(node, std::move(operands));
-            if (!id.ok()) return id.error();
-            new_id[i] = id.value();
-            continue;
+            id = result.copy_node(node, std::move(operands));
+        } else {
+            continue;  // computed inside its group's kernel
         }
-        const auto& members = groups[static_cast<std::size_t>(group_of[i])];
-        if (static_cast<NodeId>(i) != members.back()) continue;  // the root emits the whole group
-        ProgramEmitter emit(graph, new_id);
-        for (NodeId m : members) emit.member(m);
-        Result<NodeId> id = result.add_fused(emit.externals(), emit.program(), node.type, node.name);
         if (!id.ok()) return id.error();
         new_id[i] = id.value();
-        fused_ops += members.size();
     }
     for (NodeId out : graph.outputs()) {
-        Status st = result.add_output(new_id[static_cast<std::size_t>(out)]);
-        if (!st.ok()) return st.error();
+        if (Status st = result.add_output(new_id[static_cast<std::size_t>(out)]); !st.ok()) return st.error();
     }
     fill_report(report, "fuse", graph, result,
                 "fused " + std::to_string(fused_ops) + " op(s) into " + std::to_string(groups.size()) + " kernel(s)");

@@ -6,25 +6,32 @@
 A step is one enqueue of the compiled graph (every kernel of one forward
 pass over one batch of synthetic, seeded input already resident in HBM).
 The headline workload is BASELINE config 2, the fp32 MLP block
-(mlp_gelu.mcg) at B=8192: GEMM, fused bias+GELU, GEMM, fused
-bias+residual. W untimed steps, then exactly K timed steps between two HIP
-events on the executable's stream (the default W = 300, about 100 ms at
-B=8192, brings the GPU to its steady clock: it raises the clock only under
-sustained load; every other configuration warms up for WARM_SECONDS of its
-own work). Each kernel's duration is then measured
-in the same process on the same stream: the launch alone, back to back,
-between one pair of HIP events (events between launches would add their own
-gaps to short kernels).
+(mlp_gelu.mcg) at B=8192: GEMM with bias+GELU fused into its store, GEMM
+with bias+residual fused into its store. The other configurations run
+first (each after WARM_SECONDS of its own work), so the headline's W
+untimed steps and K timed steps find the GPU at its working clock; the K
+steps are timed between two HIP events on the executable's stream and are
+issued by one library call (mc_enqueue_steps), so no per-step Python work
+sits in the timed region. Each kernel's duration is then measured in the
+same process on the same stream: the launch alone, back to back, between
+one pair of HIP events. GEMM operator rows are timed from a captured HIP
+graph of back-to-back launches over rotating operand sets (no host launch
+cost; the reference times its GEMMs from a graph, bench_cuda.cpp:445-493).
+Every configuration rotates over buffer sets whose footprint exceeds twice
+the 256 MB MALL, so no timed launch reads operands the last one left on
+chip.
 
 Prints ONE JSON line. `value` is the step's GEMM throughput (TFLOP/s = the
 two GEMMs' 2MNK FLOPs per step / ms_per_step). `roofline` is for the
 kernel that takes the most time; `kernels` lists every launch with its
 algorithmic work, achieved rate and fraction of the MI355X peak (HBM 8 TB/s;
 FP32 matrix 157.3 TFLOP/s; dense bf16/fp16 2.5 PFLOP/s). `configs` adds the
-other BASELINE configs measured in the same process (skip with --quick).
-`cpu_baseline` times the CPU oracle (a C++ restatement of the reference's
-Eigen backend, test infrastructure) on a bounded row sample of the same
-workload on this host.
+other BASELINE configs measured in the same process (skip with --quick),
+each with a `cpu_baseline`: the CPU oracle (a C++ restatement of the
+reference's Eigen backend, test infrastructure) on a bounded row sample of
+that workload on this host, one thread (the reference's configuration) and
+the host's CPU share. `device.clocks` summarises the engine clock sampled
+(AMD SMI) while the headline's timed steps ran.
 """
 
 from __future__ import annotations
@@ -34,6 +41,7 @@ import json
 import os
 import statistics
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -109,131 +117,182 @@ def warm_up_for(seconds: float, batch) -> int:
     return calls
 
 
+class ClockSampler:
+    """Samples the engine clock (AMD SMI, mc_gpu_sm_clock_mhz) every few
+    milliseconds on a thread while active, as the reference records the SM
+    clock range of a run (bench/harness.hpp:264-279)."""
+
+    def __init__(self, mc, period_s: float = 0.002):
+        self.mc, self.period, self.samples = mc, period_s, []
+        self._stop = threading.Event()
+        self._thread = None
+
+    def __enter__(self):
+        def run():
+            while not self._stop.is_set():
+                v = self.mc.gpu_clock_mhz()
+                if v > 0:
+                    self.samples.append(v)
+                self._stop.wait(self.period)
+        self._thread = threading.Thread(target=run, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join()
+
+    def summary(self) -> dict:
+        x = self.samples
+        if not x:
+            return {"samples": 0}
+        return {"samples": len(x), "min_mhz": min(x), "mean_mhz": sum(x) / len(x), "max_mhz": max(x)}
+
+
+def rotation_sets(set_bytes: int) -> int:
+    """Buffer sets to cycle so that consecutive launches never find their
+    operands in the 256 MB MALL: a footprint above twice its size."""
+    return max(1, -(-2 * MALL_BYTES // max(1, set_bytes)) + 1) if set_bytes <= 2 * MALL_BYTES else 1
+
+
 def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None,
-               warm_seconds: float = 0.0) -> dict:
+               warm_seconds: float = 0.0, sampler: ClockSampler | None = None) -> dict:
     """W warmup steps (then more until `warm_seconds` have passed), then K
     steps timed between one pair of HIP events on the executable's stream
-    (ms_per_step). Then each launch of the step alone, `reps` times back to
-    back between one pair of HIP events on that stream (its mean duration,
-    with no event between launches to perturb it), in RUNS runs: the median
-    run, and the range. `rotations`: list of
-    (input_ptrs, output_ptrs) bound in turn, so consecutive launches touch
-    different buffers (defeats the 256 MB MALL)."""
-    def bind(i):
-        if rotations:
-            ins, outs = rotations[i % len(rotations)]
-            compiled.bind_inputs(ins)
-            compiled.bind_outputs(outs)
-
+    (ms_per_step); the K steps are one mc_enqueue_steps call, whose host time
+    per step is reported too. Then each launch of the step alone, `reps`
+    times back to back between one pair of HIP events on that stream (its
+    mean duration, with no event between launches to perturb it), in RUNS
+    runs: the median run, and the range. `rotations`: list of (input_ptrs,
+    output_ptrs) bound in turn, so consecutive launches touch different
+    buffers (defeats the 256 MB MALL). `sampler` runs during the K steps."""
     stream = compiled.stream
-    for i in range(warmup):
-        bind(i)
-        compiled.enqueue()
+    compiled.enqueue_steps(warmup, sets=rotations)
     compiled.synchronize()
 
     def extra():
-        for i in range(max(warmup, 10)):
-            bind(i)
-            compiled.enqueue()
+        compiled.enqueue_steps(max(warmup, 10), sets=rotations)
         compiled.synchronize()
 
     warm_up_for(warm_seconds, extra)
     start, stop = mc.Event(), mc.Event()
+    if sampler is not None:
+        sampler.__enter__()
     t0 = time.perf_counter()
     start.record(stream)
-    for i in range(steps):
-        bind(i)
-        compiled.enqueue()
+    host_us = compiled.enqueue_steps(steps, sets=rotations)
     stop.record(stream)
     compiled.synchronize()
     wall = time.perf_counter() - t0
+    if sampler is not None:
+        sampler.__exit__()
     total_ms = start.elapsed_ms(stop)
     reps = reps or max(steps, 10)
     launch_ms, launch_range = [], []
     for j in range(compiled.kernel_launches):
-        for i in range(2):
-            bind(i)
-            compiled.enqueue_launch(j)
+        compiled.enqueue_steps(2, launch=j, sets=rotations)
         runs = []
         for _ in range(RUNS):
             start.record(stream)
-            for i in range(reps):
-                bind(i)
-                compiled.enqueue_launch(j)
+            compiled.enqueue_steps(reps, launch=j, sets=rotations)
             stop.record(stream)
             compiled.synchronize()
             runs.append(start.elapsed_ms(stop) / reps)
         launch_ms.append(statistics.median(runs))
         launch_range.append([min(runs), max(runs)])
-    bind(0)
-    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "launch_ms": launch_ms,
-            "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS}
+    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "host_us_per_step": host_us,
+            "launch_ms": launch_ms, "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS}
 
 
-def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0) -> dict:
+def graph_rotation(mc, compiled, make_inputs) -> tuple[list, list]:
+    """Input/output buffer sets of `compiled` (inputs filled by
+    make_inputs()) cycled past the MALL; returns (sets, owned buffers)."""
+    set_bytes = 4 * (sum(compiled.input_sizes) + sum(compiled.output_sizes))
+    n = rotation_sets(set_bytes)
+    xs = make_inputs()
+    bufs, sets = [], []
+    for _ in range(n):
+        ins = [mc.DeviceBuffer.from_array(x) for x in xs]
+        outs = [mc.DeviceBuffer(4 * m) for m in compiled.output_sizes]
+        bufs.append((ins, outs))
+        sets.append(([b.ptr for b in ins], [b.ptr for b in outs]))
+    return sets, bufs
+
+
+def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0,
+              sampler: ClockSampler | None = None) -> dict:
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
-    t = time_graph(mc, c, steps, warmup, warm_seconds=warm_seconds)
+    # Graph replay captures once per binding: no rotation for it.
+    rot, bufs = (None, None) if options and options.get("graph") else graph_rotation(mc, c, lambda: [x])
+    t = time_graph(mc, c, steps, warmup, rot, warm_seconds=warm_seconds, sampler=sampler)
     work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
     for e, r in zip(kernels, t["launch_ms_range"]):
         e["ms_range"] = r
     flop = sum(w["flop"] for w in work if w["kind"] == "gemm")
-    return {"compiled": c, "timing": t, "kernels": kernels, "gemm_flop": flop,
-            "value": flop / (t["ms_per_step"] * 1e-3) / 1e12, "jit_ms": c.jit_compile_ms}
+    return {"compiled": c, "timing": t, "kernels": kernels, "gemm_flop": flop, "buffer_sets": len(rot) if rot else 1,
+            "value": flop / (t["ms_per_step"] * 1e-3) / 1e12, "jit_ms": c.jit_compile_ms, "buffers": bufs}
 
 
 def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, warmup: int) -> dict:
     """One fused group, rotating over input/output buffer sets whose total
     footprint exceeds twice the MALL."""
     c = mc.Compiled(path=mc.graph_path(name), dims=dims)
-    n_in, n_out = c.input_sizes[0], c.output_sizes[0]
-    set_bytes = 4 * (n_in + n_out)
-    sets = max(2, -(-2 * MALL_BYTES // set_bytes) + 1)
-    x = make_input(n_in)
-    bufs = []
-    for _ in range(sets):
-        bi, bo = mc.DeviceBuffer.from_array(x), mc.DeviceBuffer(4 * n_out)
-        bufs.append((bi, bo))
-    rot = [([bi.ptr], [bo.ptr]) for bi, bo in bufs]
+    x = make_input(c.input_sizes[0])
+    rot, bufs = graph_rotation(mc, c, lambda: [x])
     t = time_graph(mc, c, steps, warmup, rot, warm_seconds=WARM_SECONDS)
     work = node_work(c.graph(), c.launch_nodes)
     (k,) = [rate_entry(n, w, ms) for n, w, ms in zip(c.launch_names, work, t["launch_ms"])]
     k["ms_range"] = t["launch_ms_range"][0]
     k["gbs_range"] = [k["bytes"] / (ms * 1e-3) / 1e9 for ms in reversed(k["ms_range"])]
-    return {"config": name, "dims": dims, "buffer_sets": sets, "kernel": k, "ms_per_step": t["ms_per_step"],
-            "gbs": k["gbs"], "frac": k["frac"]}
+    return {"config": name, "dims": dims, "buffer_sets": len(rot), "kernel": k, "ms_per_step": t["ms_per_step"],
+            "host_us_per_step": t["host_us_per_step"], "gbs": k["gbs"], "frac": k["frac"]}
 
 
-def time_gemm(mc, launch, steps: int, warmup: int, runs_out: list | None = None) -> float:
-    """Mean duration of `steps` back-to-back launches between one pair of HIP
-    events on their stream, after `warmup` launches and a warm-up of
-    WARM_SECONDS; the median of RUNS such runs (each run's figure appended
-    to `runs_out`)."""
+def time_gemm(mc, launches, steps: int, warmup: int) -> dict:
+    """Mean duration of one launch, over `steps` back-to-back launches that
+    cycle through `launches` (one closure per operand set, each enqueueing
+    on the stream it is given), after `warmup` rounds and WARM_SECONDS of
+    warm-up. Timed two ways, RUNS runs each (median and range): `graph`, a
+    HIP graph of the `steps` launches captured once and replayed between one
+    pair of HIP events (no host launch cost, the reference's GEMM timing);
+    `direct`, the same launches issued one by one from the host."""
     s = mc.Stream()
     for _ in range(warmup):
-        launch(s)
+        for f in launches:
+            f(s)
+
+    def issue(stream):
+        for i in range(steps):
+            launches[i % len(launches)](stream)
 
     def extra():
-        for _ in range(4):
-            launch(s)
+        issue(s)
         s.synchronize()
 
     warm_up_for(WARM_SECONDS, extra)
+    g = mc.CapturedGraph(s, issue)
     start, stop = mc.Event(), mc.Event()
-    runs = []
-    for _ in range(RUNS):
-        start.record(s)
-        for _ in range(steps):
-            launch(s)
-        stop.record(s)
-        s.synchronize()
-        runs.append(start.elapsed_ms(stop) / steps)
-    if runs_out is not None:
-        runs_out.extend(runs)
-    return statistics.median(runs)
+    out = {}
+    for mode in ("graph", "direct"):
+        runs = []
+        for _ in range(RUNS):
+            start.record(s)
+            g.launch() if mode == "graph" else issue(s)
+            stop.record(s)
+            s.synchronize()
+            runs.append(start.elapsed_ms(stop) / steps)
+        out[mode] = {"ms": statistics.median(runs), "ms_range": [min(runs), max(runs)]}
+    del g
+    return out
+
+
+def operand_sets(mc, shapes_bytes: list[int], make) -> list:
+    """Operand sets (lists of device buffers from make()) enough to defeat the MALL."""
+    return [make() for _ in range(rotation_sets(sum(shapes_bytes)))]
 
 
 def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]:
@@ -241,37 +300,45 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
     for m, n, k in shapes:
         kernel = mc.resolve_matmul_kernel("auto", m, n, k, cus)
         splits = mc.matmul_splits(kernel, m, n, k, cus)
-        a = mc.DeviceBuffer.from_array(mc.uniform(m * k, 1, -1.0, 1.0))
-        b = mc.DeviceBuffer.from_array(mc.uniform(k * n, 2, -1.0, 1.0))
-        c = mc.DeviceBuffer(4 * m * n)
         ws_bytes = mc.matmul_workspace_bytes(kernel, m, n, splits)
-        ws = mc.DeviceBuffer(ws_bytes) if ws_bytes else None
-        runs = []
-        ms = time_gemm(mc, lambda s: mc.launch_matmul(kernel, a.ptr, b.ptr, c.ptr, m, n, k, s, splits,
-                                                       ws.ptr if ws else None), steps, warmup, runs)
+        a_host, b_host = mc.uniform(m * k, 1, -1.0, 1.0), mc.uniform(k * n, 2, -1.0, 1.0)
+        sets = operand_sets(mc, [4 * m * k, 4 * k * n, 4 * m * n, ws_bytes],
+                            lambda: (mc.DeviceBuffer.from_array(a_host), mc.DeviceBuffer.from_array(b_host),
+                                     mc.DeviceBuffer(4 * m * n), mc.DeviceBuffer(ws_bytes) if ws_bytes else None))
+        launches = [lambda st, a=a, b=b, c=c, ws=ws: mc.launch_matmul(kernel, a.ptr, b.ptr, c.ptr, m, n, k, st, splits,
+                                                                     ws.ptr if ws else None)
+                    for a, b, c, ws in sets]
+        t = time_gemm(mc, launches, steps, warmup)
+        ms = t["graph"]["ms"]
         flop = 2.0 * m * n * k
-        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "ms": ms, "ms_range": [min(runs), max(runs)],
-             "tflops": flop / (ms * 1e-3) / 1e12}
+        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "operand_sets": len(sets), "ms": ms,
+             "ms_range": t["graph"]["ms_range"], "timing": "hip graph of back-to-back launches",
+             "ms_direct_launches": t["direct"]["ms"], "tflops": flop / (ms * 1e-3) / 1e12}
         e["frac"] = e["tflops"] / PEAK_FP32_TFLOPS
-        if m == 16:  # HBM-bound skinny shape: report bytes too
+        if m <= 32:  # HBM-bound skinny shape: report bytes too
             byt = 4.0 * (m * k + k * n + m * n)
+            e["bytes"] = byt
             e["gbs"] = byt / (ms * 1e-3) / 1e9
             e["frac_hbm"] = e["gbs"] / PEAK_HBM_GBS
+        n_sets = len(sets)
+        del sets, launches
         if splits > 1 or m <= 32:
             # The same product as a one-matmul graph compiled with autotune=1
             # (split count and tile configuration timed at compile time).
             g = mc.Compiled(f"graph gemm\ninput a : f32[{m}, {k}]\ninput b : f32[{k}, {n}]\nc = matmul a, b\n"
                             f"output c\n", options={"autotune": 1})
-            g.upload([mc.uniform(m * k, 1, -1.0, 1.0), mc.uniform(k * n, 2, -1.0, 1.0)])
-            t = time_graph(mc, g, steps, warmup, warm_seconds=WARM_SECONDS)
-            tms = t["launch_ms"][0]
-            e["autotuned"] = {"ms": tms, "ms_range": t["launch_ms_range"][0], "kernel": g.matmul_kernels[0],
-                              "tflops": flop / (tms * 1e-3) / 1e12}
+            rot, bufs = graph_rotation(mc, g, lambda: [a_host, b_host])
+            tg = time_graph(mc, g, steps, warmup, rot, warm_seconds=WARM_SECONDS)
+            tms = tg["launch_ms"][0]
+            e["autotuned"] = {"ms": tms, "ms_range": tg["launch_ms_range"][0], "kernel": g.matmul_kernels[0],
+                              "launch": g.launch_names[0], "tflops": flop / (tms * 1e-3) / 1e12}
             g.close()
-            log(f"gemm fp32 {m}x{n}x{k} autotuned ({e['autotuned']['kernel']}): {tms:.3f} ms "
+            del bufs
+            log(f"gemm fp32 {m}x{n}x{k} autotuned ({e['autotuned']['launch']}): {tms:.4f} ms "
                 f"{e['autotuned']['tflops']:.1f} TFLOP/s")
         out.append(e)
-        log(f"gemm fp32 {m}x{n}x{k} {kernel}: {ms:.3f} ms {e['tflops']:.1f} TFLOP/s")
+        log(f"gemm fp32 {m}x{n}x{k} {kernel} splits={splits}: {ms:.4f} ms {e['tflops']:.1f} TFLOP/s "
+            f"(direct launches {t['direct']['ms']:.4f} ms), {n_sets} operand sets")
     return out
 
 
@@ -281,83 +348,156 @@ def bench_gemm_lowp(mc, shapes, steps: int, warmup: int) -> list[dict]:
         a32 = mc.DeviceBuffer.from_array(mc.uniform(m * k, 1, -1.0, 1.0))
         b32 = mc.DeviceBuffer.from_array(mc.uniform(k * n, 2, -1.0, 1.0))
         for kernel, dtype in (("tensor_core_bf16", mc.DTYPE_BF16), ("tensor_core_f16", mc.DTYPE_F16)):
-            a, b = mc.DeviceBuffer(2 * m * k), mc.DeviceBuffer(2 * k * n)
-            mc.convert_f32(dtype, a32.ptr, a.ptr, m * k)
-            mc.convert_f32(dtype, b32.ptr, b.ptr, k * n)
-            c = mc.DeviceBuffer(4 * m * n)
-            runs = []
-            ms = time_gemm(mc, lambda s: mc.launch_matmul_lowp(kernel, dtype, a.ptr, b.ptr, c.ptr, m, n, k, s),
-                           steps, warmup, runs)
+            def make():
+                a, b = mc.DeviceBuffer(2 * m * k), mc.DeviceBuffer(2 * k * n)
+                mc.convert_f32(dtype, a32.ptr, a.ptr, m * k)
+                mc.convert_f32(dtype, b32.ptr, b.ptr, k * n)
+                return a, b, mc.DeviceBuffer(4 * m * n)
+            sets = operand_sets(mc, [2 * m * k, 2 * k * n, 4 * m * n], make)
+            launches = [lambda st, a=a, b=b, c=c: mc.launch_matmul_lowp(kernel, dtype, a.ptr, b.ptr, c.ptr, m, n, k, st)
+                        for a, b, c in sets]
+            t = time_gemm(mc, launches, steps, warmup)
+            ms = t["graph"]["ms"]
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
             out.append({"m": m, "n": n, "k": k, "kernel": kernel, "inputs": "bf16" if dtype == 1 else "fp16",
-                        "ms": ms, "ms_range": [min(runs), max(runs)], "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
-            log(f"gemm {kernel} {m}x{n}x{k}: {ms:.3f} ms {tf:.1f} TFLOP/s")
-            del a, b, c
+                        "operand_sets": len(sets), "ms": ms, "ms_range": t["graph"]["ms_range"],
+                        "ms_direct_launches": t["direct"]["ms"], "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
+            log(f"gemm {kernel} {m}x{n}x{k}: {ms:.3f} ms {tf:.1f} TFLOP/s ({len(sets)} operand sets)")
+            del sets, launches
     return out
 
 
 def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
     """BASELINE config 5 with its epilogue: matmul_bias_gelu.mcg (y =
     gelu_tanh(x w + bias), fp32 in and out) compiled with the bf16 / fp16
-    matrix-core kernel. A step is one launch: it rounds x to 16 bits (w was
-    rounded once, at compile time), then runs the GEMM with bias+GELU fused
-    into its store; `gemm_epilogue_tflops` counts the GEMM's 2MNK FLOPs over
-    that whole launch, the rounding of x included (about 0.1 ms at 8192^2)."""
+    matrix-core kernel. A step rounds x to 16 bits (w was rounded once, at
+    compile time), then runs the GEMM with bias+GELU fused into its store;
+    `gemm_epilogue_tflops` counts the GEMM's 2MNK FLOPs over the fused
+    GEMM launch alone."""
     out = []
     for m, n, k in shapes:
+        x = mc.uniform(m * k, 1, -1.0, 1.0)
         for kernel in ("tensor_core_bf16", "tensor_core_f16"):
             c = mc.Compiled(path=mc.graph_path("matmul_bias_gelu"), dims={"M": m, "K": k, "N": n},
                             options={"matmul": kernel})
-            c.upload([mc.uniform(m * k, 1, -1.0, 1.0)])
-            t = time_graph(mc, c, steps, warmup, warm_seconds=WARM_SECONDS)
+            rot, bufs = graph_rotation(mc, c, lambda: [x])
+            t = time_graph(mc, c, steps, warmup, rot, warm_seconds=WARM_SECONDS)
             names = c.launch_names
             (j,) = [i for i, nm in enumerate(names) if nm.startswith("matmul")]
             gemm_ms = t["launch_ms"][j]
             tf = 2.0 * m * n * k / (gemm_ms * 1e-3) / 1e12
-            out.append({"m": m, "n": n, "k": k, "kernel": kernel, "launches": names,
+            out.append({"m": m, "n": n, "k": k, "kernel": kernel, "launches": names, "buffer_sets": len(rot),
                         "ms_per_step": t["ms_per_step"], "gemm_epilogue_ms": gemm_ms, "gemm_epilogue_tflops": tf,
                         "frac": tf / PEAK_BF16_TFLOPS, "launch_ms": t["launch_ms"]})
             log(f"{kernel} {m}x{n}x{k} + bias + gelu: step {t['ms_per_step']:.3f} ms, fused GEMM launch "
                 f"{gemm_ms:.3f} ms {tf:.1f} TFLOP/s")
-            del c
+            del c, bufs
     return out
 
 
-def cpu_baseline(batch_rows: int, seconds: float) -> dict:
-    """The CPU oracle (restating the reference's Eigen backend) on the first
-    `batch_rows` rows of the MLP workload, one thread, repeated for about
-    `seconds`. Throughput in the headline unit."""
-    import minicompiler_amd as mc
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_threads() -> int:
+    """This GPU's share of the host (at most 16 threads per GPU on the box)."""
+    return max(1, min(os.cpu_count() or 1, 16))
+
+
+def cpu_time(call, seconds: float, min_reps: int = 3) -> tuple[float, int]:
+    """The reference's time_cpu (bench/harness.hpp:67-79): one warm-up call,
+    then calls until `seconds` have passed (at least min_reps); the median
+    call time and the number of calls."""
+    call()
+    times, until = [], time.perf_counter() + seconds
+    while len(times) < min_reps or time.perf_counter() < until:
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def sample_rows(full: int, first: int, per_call, target_s: float = 0.25) -> int:
+    """Rows of the workload for one CPU call of about target_s: per_call(r)
+    runs r rows once; a first call with `first` rows sets the scale."""
+    t0 = time.perf_counter()
+    per_call(first)
+    el = max(time.perf_counter() - t0, 1e-4)
+    return int(max(1, min(full, round(first * target_s / el))))
+
+
+def cpu_entry(per_row_work: float, unit: str, rows: int, full_rows: int, call, what: str,
+              seconds: float) -> dict:
+    """One and all-threads timings of call() (rows of the workload), as the
+    throughput of `per_row_work` units per row."""
     from oracle import oracle as orc
 
-    c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch_rows}, backend="none")
-    g = c.graph()
-    consts = {n["id"]: c.constant(n["id"]) for n in g["nodes"] if n["op_name"] == "const"}
-    x = mc.uniform(batch_rows * 512, 1, -1.0, 1.0)
-    flop = 4.0 * batch_rows * 512 * 2048
-
-    def timed(threads: int, secs: float):
+    out = {}
+    for threads, secs in ((1, seconds), (cpu_threads(), seconds / 2)):
         orc.set_threads(threads)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            orc.evaluate(g, consts, [x])
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= secs and reps >= 2:
-                break
-        return el / reps, reps
-
-    per, reps = timed(1, seconds)
-    # The reference publishes one thread; all of this GPU's host share too (at
-    # most 16 threads: the box's CPU share per GPU), rows split over threads.
-    threads = max(1, min(os.cpu_count() or 1, 16))
-    per_all, reps_all = timed(threads, seconds / 2)
+        per, reps = cpu_time(call, secs)
+        out[threads] = (per_row_work * rows / per / (1e12 if unit == "TFLOP/s" else 1e9), per, reps)
     orc.set_threads(1)
-    return {"value": flop / per / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"mlp_gelu rows 0..{batch_rows - 1} of the B=8192 batch, {reps} reps, {per * 1e3:.1f} ms/rep, "
-                      f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM), 1 thread, {os.cpu_count()} host cores",
-            "all_cores": {"value": flop / per_all / 1e12, "threads": threads,
-                          "sample": f"the same rows, {reps_all} reps, {per_all * 1e3:.1f} ms/rep"}}
+    v1, per1, reps1 = out[1]
+    va, pera, repsa = out[cpu_threads()]
+    return {"value": v1, "unit": unit, "cores": 1, "threads": 1, "kind": "port",
+            "sample": f"{what}: rows 0..{rows - 1} of {full_rows}, {reps1} calls, median {per1 * 1e3:.2f} ms/call, "
+                      f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM; Eigen is not on the box), "
+                      f"1 thread, {os.cpu_count()} host cores",
+            "all_cores": {"value": va, "threads": cpu_threads(),
+                          "sample": f"the same rows, {repsa} calls, median {pera * 1e3:.2f} ms/call"}}
+
+
+def cpu_baseline_graph(mc, name: str, dims_of, full_rows: int, row_elems: int, make_input, per_row_work: float,
+                       unit: str, first: int, seconds: float) -> dict:
+    """The oracle evaluating graph `name` on its first rows (rows are
+    independent in every bench graph: elementwise groups and x·W products)."""
+    from oracle import oracle as orc
+
+    cache = {}
+
+    def prepared(rows):
+        if rows not in cache:
+            c = mc.Compiled(path=mc.graph_path(name), dims=dims_of(rows), backend="none")
+            g = c.graph()
+            consts = {nd["id"]: c.constant(nd["id"]) for nd in g["nodes"] if nd["op_name"] == "const"}
+            cache.clear()
+            cache[rows] = (g, consts, make_input(rows * row_elems))
+        return cache[rows]
+
+    def run(rows):
+        g, consts, x = prepared(rows)
+        orc.evaluate(g, consts, [x])
+
+    orc.set_threads(1)
+    prepared(first)
+    rows = sample_rows(full_rows, first, run)
+    prepared(rows)
+    return cpu_entry(per_row_work, unit, rows, full_rows, lambda: run(rows), f"{name} {dims_of(full_rows)}", seconds)
+
+
+def cpu_baseline_gemm(mc, m: int, n: int, k: int, seconds: float, what: str = "") -> dict:
+    """The oracle's fp32 GEMM (the reference's Eigen CPU backend has no 16-bit
+    GEMM; config 5 is checked against, and compared with, its fp32 GEMM) on
+    the first rows of A."""
+    from oracle import oracle as orc
+
+    b = mc.uniform(k * n, 2, -1.0, 1.0)
+    a_full_rows = min(m, 4096)
+    a = mc.uniform(a_full_rows * k, 1, -1.0, 1.0)
+    orc.set_threads(1)
+    run = lambda r: orc.matmul(a[:r * k], b, r, k, n)
+    rows = sample_rows(min(m, a_full_rows), min(m, 4), run)
+    return cpu_entry(2.0 * n * k, "TFLOP/s", rows, m, lambda: run(rows), what or f"fp32 gemm {m}x{n}x{k}", seconds)
+
+
+def cpu_baseline(batch_rows: int, seconds: float) -> dict:
+    """The headline's CPU baseline: the oracle on the first `batch_rows` rows
+    of the MLP workload, one thread, repeated for about `seconds` (and the
+    host's CPU share for half as long). Throughput in the headline unit."""
+    import minicompiler_amd as mc
+
+    e = cpu_baseline_graph(mc, "mlp_gelu", lambda r: {"B": r}, 8192, 512, lambda n: mc.uniform(n, 1, -1.0, 1.0),
+                           4.0 * 512 * 2048, "TFLOP/s", batch_rows, seconds)
+    return e
 
 
 def measured_traffic(workload: str, launch: str):
@@ -372,11 +512,86 @@ def measured_traffic(workload: str, launch: str):
     return None if entry is None else entry["traffic_bytes"]
 
 
+FP32_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384),
+               (16, 4096, 4096)]
+LOWP_SHAPES = [(8192, 8192, 8192), (4096, 14336, 4096)]
+
+
+def run_configs(mc, args, cus: int, line: dict, cpu_s: float) -> None:
+    """BASELINE's other configs, each with its CPU baseline (cpu_s seconds
+    of one-thread CPU work, half that on all threads; 0: none)."""
+    cfgs = line.setdefault("configs", {})
+    want = lambda w: args.workload == w or (args.workload == "mlp" and not args.quick)
+    if want("gelu"):
+        e = bench_elementwise_graph(mc, "gelu_chain", {"M": 4096, "N": 4096}, lambda n: mc.uniform(n, 1, -3.0, 3.0),
+                                    args.steps, args.warmup)
+        if cpu_s:
+            e["cpu_baseline"] = cpu_baseline_graph(mc, "gelu_chain", lambda r: {"M": r, "N": 4096}, 4096, 4096,
+                                                   lambda n: mc.uniform(n, 1, -3.0, 3.0), 8.0 * 4096, "GB/s", 16, cpu_s)
+        cfgs["gelu_4096x4096"] = e
+        log(f"gelu: {e['gbs']:.0f} GB/s, host {e['host_us_per_step']:.1f} us/step")
+    if want("batchnorm"):
+        e = bench_elementwise_graph(mc, "batchnorm_relu", {"R": 200704, "C": 256},
+                                    lambda n: mc.normal(n, 1, 0.0, 1.0), args.steps, args.warmup)
+        if cpu_s:
+            e["cpu_baseline"] = cpu_baseline_graph(mc, "batchnorm_relu", lambda r: {"R": r, "C": 256}, 200704, 256,
+                                                   lambda n: mc.normal(n, 1, 0.0, 1.0), 8.0 * 256, "GB/s", 256, cpu_s)
+        cfgs["batchnorm_relu_200704x256"] = e
+        log(f"batchnorm: {e['gbs']:.0f} GB/s, host {e['host_us_per_step']:.1f} us/step")
+    if args.workload == "mlp" and not args.quick:
+        # BASELINE config 2's batch sweep: the small batches are timed with
+        # direct launches, with hipGraph replay, and with the split count and
+        # tile configuration autotuned at compile time (autotune=1). Rows are
+        # independent, so the headline's CPU baseline (per row) covers them.
+        for b in (256, 1024):
+            entry = {}
+            for mode, opts in (("direct", None), ("graph_replay", {"graph": 1}), ("autotuned", {"autotune": 1})):
+                r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts, WARM_SECONDS)
+                entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
+                               "launches": r["compiled"].kernel_launches, "buffer_sets": r["buffer_sets"],
+                               "host_us_per_step": r["timing"]["host_us_per_step"],
+                               "launch_ms": r["timing"]["launch_ms"]}
+                del r
+            entry["cpu_baseline"] = "the headline's cpu_baseline (mlp_gelu rows; rows are independent)"
+            cfgs[f"mlp_b{b}"] = entry
+            log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
+                f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step, "
+                f"autotuned {entry['autotuned']['ms_per_step'] * 1e3:.1f} us/step")
+    cpu_gemm = {}
+    if want("gemm_fp32"):
+        g = bench_gemm_fp32(mc, cus, FP32_SHAPES, 20, 2)  # plus WARM_SECONDS per shape
+        for e in g:
+            if cpu_s:
+                key = (e["m"], e["n"], e["k"])
+                cpu_gemm[key] = e["cpu_baseline"] = cpu_baseline_gemm(mc, *key, cpu_s)
+        cfgs["gemm_fp32"] = g
+    if want("gemm_bf16"):
+        g = bench_gemm_lowp(mc, LOWP_SHAPES, 20, 2)  # plus WARM_SECONDS
+        for e in g:
+            if cpu_s:
+                key = (e["m"], e["n"], e["k"])
+                if key not in cpu_gemm:
+                    cpu_gemm[key] = cpu_baseline_gemm(mc, *key, cpu_s)
+                e["cpu_baseline"] = cpu_gemm[key]
+        cfgs["gemm_bf16_fp16"] = g
+        ep = bench_lowp_epilogue(mc, LOWP_SHAPES, 20, 2)
+        cpu_ep = {}
+        for e in ep:
+            if cpu_s:
+                m, n, k = e["m"], e["n"], e["k"]
+                if (m, n, k) not in cpu_ep:
+                    cpu_ep[(m, n, k)] = cpu_baseline_graph(
+                        mc, "matmul_bias_gelu", lambda r, k=k, n=n: {"M": r, "K": k, "N": n}, m, k,
+                        lambda cnt: mc.uniform(cnt, 1, -1.0, 1.0), 2.0 * n * k, "TFLOP/s", 2, cpu_s)
+                e["cpu_baseline"] = cpu_ep[(m, n, k)]
+        cfgs["gemm_bf16_fp16_bias_gelu"] = ep
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     # About 70 ms of timed work at B=8192; the 300 warmup steps (about 100 ms)
-    # bring the GPU to its steady clock first.
+    # keep the GPU at its working clock first.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="mlp",
@@ -384,7 +599,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=8192)
     ap.add_argument("--quick", action="store_true", help="headline workload only (no other configs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the headline's CPU baseline")
+    ap.add_argument("--config-cpu-seconds", type=float, default=1.5, help="each other config's CPU baseline")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -396,19 +612,28 @@ def main() -> int:
 
     dev = mc.device_json()
     cus = dev["cu_count"]
-    log(f"device: {dev['name']} {dev['arch']} CUs={cus} clock={dev['clock_mhz']} MHz")
+    log(f"device: {dev['name']} {dev['arch']} CUs={cus} clock={dev['clock_mhz']} MHz "
+        f"(now {dev.get('clock_now_mhz', 0):.0f} MHz)")
     line = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded splitmix64 uniform/normal, "
                                                             "random-init constants of the graph)"}
+    cpu_s = 0.0 if args.no_cpu_baseline else args.config_cpu_seconds
+    whole = ClockSampler(mc, period_s=0.05)
+    with whole:
+        run_configs(mc, args, cus, line, cpu_s)
+    cfgs = line.get("configs", {})
+    sampler = ClockSampler(mc)
 
     if args.workload == "mlp":
-        r = bench_mlp(mc, args.batch, args.steps, args.warmup)
+        r = bench_mlp(mc, args.batch, args.steps, args.warmup, sampler=sampler)
         ks = r["kernels"]
         dom = max(ks, key=lambda e: e["ms"])
         line.update({"value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["timing"]["ms_per_step"],
                      "dtype": "f32",
                      "config": {"workload": f"mlp_gelu B={args.batch} D=512 H=2048 fp32 (BASELINE config 2)",
-                                "global_batch": args.batch, "matmul": ",".join(r["compiled"].matmul_kernels)}})
+                                "global_batch": args.batch, "matmul": ",".join(r["compiled"].matmul_kernels),
+                                "buffer_sets": r["buffer_sets"]},
+                     "host_us_per_step": r["timing"]["host_us_per_step"]})
         unit = "TFLOP/s" if dom["bound"] == "mfma" else "GB/s"
         achieved = dom["tflops"] if dom["bound"] == "mfma" else dom["gbs"]
         line["roofline"] = {"bound": dom["bound"], "kernel": dom["launch"], "achieved": achieved,
@@ -417,74 +642,47 @@ def main() -> int:
         fused = [k for k in ks if k["bound"] == "hbm"]
         line["fused_gbs"] = sum(k["bytes"] for k in fused) / (sum(k["ms"] for k in fused) * 1e-3) / 1e9 if fused else None
         line["jit_compile_ms"] = r["jit_ms"]
-    else:
-        line["unit"] = "GB/s" if args.workload in ("gelu", "batchnorm") else "TFLOP/s"
-
-    if args.workload == "copy":
+    elif args.workload == "copy":
         # Byte-counter calibration: reads and writes 128 MiB each, known exactly.
         k = bench_elementwise_graph(mc, "copy_neg", {"M": 8192, "N": 4096}, lambda n: mc.uniform(n, 1, -1.0, 1.0),
                                     args.steps, args.warmup)
-        line.update({"value": k["gbs"], "ms_per_step": k["ms_per_step"], "dtype": "f32",
+        line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",
                      "config": {"workload": "copy_neg (counter calibration)", **k["dims"]},
                      "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
-    if args.workload in ("gelu", "batchnorm") or (args.workload == "mlp" and not args.quick):
-        cfgs = line.setdefault("configs", {})
-        if args.workload != "batchnorm":
-            cfgs["gelu_4096x4096"] = bench_elementwise_graph(
-                mc, "gelu_chain", {"M": 4096, "N": 4096}, lambda n: mc.uniform(n, 1, -3.0, 3.0), args.steps, args.warmup)
-            log(f"gelu: {cfgs['gelu_4096x4096']['gbs']:.0f} GB/s")
-        if args.workload != "gelu":
-            cfgs["batchnorm_relu_200704x256"] = bench_elementwise_graph(
-                mc, "batchnorm_relu", {"R": 200704, "C": 256}, lambda n: mc.normal(n, 1, 0.0, 1.0), args.steps,
-                args.warmup)
-            log(f"batchnorm: {cfgs['batchnorm_relu_200704x256']['gbs']:.0f} GB/s")
-        if args.workload in ("gelu", "batchnorm"):
-            k = next(iter(cfgs.values()))
-            line.update({"value": k["gbs"], "ms_per_step": k["ms_per_step"], "dtype": "f32",
-                         "config": {"workload": k["config"], **k["dims"]},
-                         "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
-                                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
-    if args.workload == "mlp" and not args.quick:
-        # BASELINE config 2's batch sweep: the small batches are timed with
-        # direct launches, with hipGraph replay, and with the split count and
-        # tile configuration autotuned at compile time (autotune=1).
-        cfgs = line.setdefault("configs", {})
-        for b in (256, 1024):
-            entry = {}
-            for mode, opts in (("direct", None), ("graph_replay", {"graph": 1}), ("autotuned", {"autotune": 1})):
-                r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts, WARM_SECONDS)
-                entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
-                               "launches": r["compiled"].kernel_launches}
-            cfgs[f"mlp_b{b}"] = entry
-            log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
-                f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step, "
-                f"autotuned {entry['autotuned']['ms_per_step'] * 1e3:.1f} us/step")
-    if args.workload == "gemm_fp32" or (args.workload == "mlp" and not args.quick):
-        shapes = [(1024, 1024, 1024), (4096, 4096, 4096), (8192, 8192, 8192), (256, 256, 16384), (16, 4096, 4096)]
-        g = bench_gemm_fp32(mc, cus, shapes, 10, 3)  # plus WARM_SECONDS per shape
-        line.setdefault("configs", {})["gemm_fp32"] = g
-        if args.workload == "gemm_fp32":
-            top = g[2]
-            line.update({"value": top["tflops"], "ms_per_step": top["ms"], "dtype": "f32",
-                         "config": {"workload": "fp32 gemm 8192^3 (BASELINE config 4)"},
-                         "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
-                                      "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
-    if args.workload == "gemm_bf16" or (args.workload == "mlp" and not args.quick):
-        g = bench_gemm_lowp(mc, [(8192, 8192, 8192), (4096, 14336, 4096)], 20, 3)  # plus WARM_SECONDS
-        line.setdefault("configs", {})["gemm_bf16_fp16"] = g
-        line["configs"]["gemm_bf16_fp16_bias_gelu"] = bench_lowp_epilogue(
-            mc, [(8192, 8192, 8192), (4096, 14336, 4096)], 20, 3)
-        if args.workload == "gemm_bf16":
-            top = g[0]
-            line.update({"value": top["tflops"], "ms_per_step": top["ms"], "dtype": "bf16",
-                         "config": {"workload": "bf16 gemm 8192^3, bf16 inputs in HBM (BASELINE config 5)"},
-                         "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
-                                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
+    elif args.workload in ("gelu", "batchnorm"):
+        k = next(iter(cfgs.values()))
+        line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",
+                     "config": {"workload": k["config"], **k["dims"]},
+                     "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
+                                  "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
+        if "cpu_baseline" in k:
+            line["cpu_baseline"] = k["cpu_baseline"]
+    elif args.workload == "gemm_fp32":
+        top = cfgs["gemm_fp32"][3]
+        line.update({"value": top["tflops"], "unit": "TFLOP/s", "ms_per_step": top["ms"], "dtype": "f32",
+                     "config": {"workload": "fp32 gemm 8192^3 (BASELINE config 4)"},
+                     "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
+                                  "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
+        if "cpu_baseline" in top:
+            line["cpu_baseline"] = top["cpu_baseline"]
+    elif args.workload == "gemm_bf16":
+        top = cfgs["gemm_bf16_fp16"][0]
+        line.update({"value": top["tflops"], "unit": "TFLOP/s", "ms_per_step": top["ms"], "dtype": "bf16",
+                     "config": {"workload": "bf16 gemm 8192^3, bf16 inputs in HBM (BASELINE config 5)"},
+                     "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
+                                  "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
+        if "cpu_baseline" in top:
+            line["cpu_baseline"] = top["cpu_baseline"]
 
     if "roofline" in line:
         line["roofline"]["traffic"] = measured_traffic(line["config"]["workload"], line["roofline"]["kernel"])
-    line["device"] = {k: dev[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
+    d = mc.device_json(sampler.samples)
+    line["device"] = {k: d[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
+    line["device"]["clocks"] = {**d["clocks"], "during": "the headline's timed steps",
+                                "source": "AMD SMI current GFX clock (mean over XCDs), sampled every 2 ms"}
+    line["device"]["clocks_configs"] = {**whole.summary(), "during": "the other configs (GPU and CPU work)",
+                                        "period_ms": 50}
     if not args.no_cpu_baseline and args.workload == "mlp":
         line["cpu_baseline"] = cpu_baseline(256, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -59,7 +59,9 @@ MC_API int mc_kernel_launches(void* handle);
 /* The matmul kernel of each matmul, comma-separated, truncated to `size`.
  * Returns 0, or 1 without an executable (not a length: capi.cpp:184-202). */
 MC_API int mc_matmul_kernels(void* handle, char* out, int size);
-/* Engine clock in MHz as the runtime reports it, 0 without a device. (capi.cpp:204-210) */
+/* The engine clock right now in MHz (AMD SMI's current GFX clock of device
+ * 0; the reference reads NVML's SM clock), 0 when it cannot be read.
+ * (capi.cpp:204-210) */
 MC_API double mc_gpu_sm_clock_mhz(void);
 /* JSON description of device 0 (name, arch, CUs, clocks, bus, peaks) with the
  * `clocks` samples summarised. 0 ok, 1 no device, 2 `out` too small.
@@ -113,6 +115,15 @@ MC_API int mc_launch_names(void* handle, char* out, int size);
 /* Launch j of the executable's launch list alone on `stream` (NULL: its own
  * stream), e.g. to time one kernel back to back without events between. */
 MC_API int mc_enqueue_launch(void* handle, int j, void* stream);
+/* `steps` enqueues in one call, for timing loops with no per-step host
+ * work outside the library: step i first binds buffer set i % sets (when
+ * sets > 0; set r's inputs at set_inputs[r * num_inputs ...], its outputs
+ * at set_outputs[r * num_outputs ...], as mc_bind_inputs / mc_bind_outputs
+ * take them; the last set used stays bound), then enqueues the whole step
+ * (launch = -1) or only launch `launch` on `stream`. *host_us_per_step
+ * (if not NULL) receives the host time per step of the loop. */
+MC_API int mc_enqueue_steps(void* handle, int launch, int steps, int sets, const void* const* set_inputs,
+                            void* const* set_outputs, void* stream, double* host_us_per_step);
 /* The graph nodes each launch computes, launches separated by ';' and nodes
  * by ',' (a matmul with a fused epilogue lists the matmul, then the group). */
 MC_API int mc_launch_nodes(void* handle, char* out, int size);
@@ -218,6 +229,15 @@ MC_API int mc_event_create(void** event);
 MC_API int mc_event_destroy(void* event);
 MC_API int mc_event_record(void* event, void* stream);
 MC_API int mc_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Stream capture into a HIP graph, e.g. to time launches without host
+ * launch cost (the reference times its GEMMs from a captured graph,
+ * bench/bench_cuda.cpp:445-493): launches enqueued on `stream` between the
+ * two calls are recorded, not run; mc_stream_end_capture instantiates them
+ * (*graph_exec; NULL on failure, and capture has ended either way). */
+MC_API int mc_stream_begin_capture(void* stream);
+MC_API int mc_stream_end_capture(void* stream, void** graph_exec);
+MC_API int mc_graph_launch(void* graph_exec, void* stream);
+MC_API int mc_graph_destroy(void* graph_exec);
 MC_API const char* mc_error_string(int code);
 
 #ifdef __cplusplus

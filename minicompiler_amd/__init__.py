@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mc_profile_start": (_i, [_vp, _i]),
     "mc_enqueue_profiled": (_i, [_vp, _vp]),
     "mc_enqueue_launch": (_i, [_vp, _i, _vp]),
+    "mc_enqueue_steps": (_i, [_vp, _i, _i, _i, _c.POINTER(_vp), _c.POINTER(_vp), _vp, _c.POINTER(_d)]),
     "mc_launch_nodes": (_i, [_vp, _cp, _i]),
     "mc_profile_read": (_i, [_vp, _fp, _i]),
     "mc_launch_names": (_i, [_vp, _cp, _i]),
@@ -125,6 +126,10 @@ _SIGNATURES = {
     "mc_event_destroy": (_i, [_vp]),
     "mc_event_record": (_i, [_vp, _vp]),
     "mc_event_elapsed_ms": (_i, [_vp, _vp, _c.POINTER(_f)]),
+    "mc_stream_begin_capture": (_i, [_vp]),
+    "mc_stream_end_capture": (_i, [_vp, _c.POINTER(_vp)]),
+    "mc_graph_launch": (_i, [_vp, _vp]),
+    "mc_graph_destroy": (_i, [_vp]),
     "mc_error_string": (_cp, [_i]),
 }
 
@@ -281,6 +286,38 @@ class Event:
             pass
 
 
+class CapturedGraph:
+    """The launches `record(stream)` enqueues on `stream`, captured into a HIP
+    graph (nothing runs while recording); launch() replays them."""
+
+    def __init__(self, stream: "Stream", record):
+        lib = library()
+        _check(lib.mc_stream_begin_capture(stream.handle), "hipStreamBeginCapture")
+        try:
+            record(stream)
+        finally:
+            p = ctypes.c_void_p()
+            rc = lib.mc_stream_end_capture(stream.handle, ctypes.byref(p))
+        _check(rc, "hipStreamEndCapture / hipGraphInstantiate")
+        self.handle = p.value
+        self.stream = stream
+
+    def launch(self) -> None:
+        _check(library().mc_graph_launch(self.handle, self.stream.handle), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if self.handle:
+                library().mc_graph_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def gpu_clock_mhz() -> float:
+    """The engine clock of device 0 right now (AMD SMI), 0 if unreadable."""
+    return float(library().mc_gpu_sm_clock_mhz())
+
+
 def _stream_handle(stream):
     return stream.handle if isinstance(stream, Stream) else stream
 
@@ -390,6 +427,20 @@ class Compiled:
 
     def enqueue_launch(self, j: int, stream=None) -> None:
         _check_graph(library().mc_enqueue_launch(self._h, j, _stream_handle(stream)), "mc_enqueue_launch")
+
+    def enqueue_steps(self, steps: int, launch: int = -1, sets=None, stream=None) -> float:
+        """`steps` enqueues in one library call (launch -1: the whole step,
+        else launch `launch` alone), binding buffer set i % len(sets) before
+        step i when `sets` (a list of (input_ptrs, output_ptrs)) is given.
+        Returns the host microseconds per step of the loop."""
+        ni, no = self.num_inputs, self.num_outputs
+        n = len(sets) if sets else 0
+        ip = (ctypes.c_void_p * max(1, n * ni))(*[p for ins, _ in (sets or []) for p in ins])
+        op = (ctypes.c_void_p * max(1, n * no))(*[p for _, outs in (sets or []) for p in outs])
+        us = ctypes.c_double()
+        _check_graph(library().mc_enqueue_steps(self._h, launch, steps, n, ip, op, _stream_handle(stream),
+                                                ctypes.byref(us)), "mc_enqueue_steps")
+        return float(us.value)
 
     def enqueue_profiled(self, stream=None) -> None:
         _check_graph(library().mc_enqueue_profiled(self._h, _stream_handle(stream)), "mc_enqueue_profiled")

@@ -16,6 +16,7 @@
 #include "minicompiler/runtime/memory_plan.hpp"
 
 #include <cerrno>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -414,6 +415,43 @@ MC_API int mc_enqueue_launch(void* h, int j, void* stream) {
     return st.ok() ? 0 : fail(st.message());
 }
 
+MC_API int mc_enqueue_steps(void* h, int launch, int steps, int sets, const void* const* set_inputs,
+                            void* const* set_outputs, void* stream, double* host_us_per_step) {
+    Compiled* c = as_compiled(h);
+    if (!c->exe) return fail("mc_enqueue_steps: no executable");
+    if (steps < 0 || sets < 0 || (sets > 0 && (set_inputs == nullptr || set_outputs == nullptr))) {
+        return fail("mc_enqueue_steps: bad step or buffer-set arguments");
+    }
+    if (launch >= static_cast<int>(c->exe->kernel_launches())) {
+        return fail("mc_enqueue_steps: launch " + std::to_string(launch) + " out of range");
+    }
+    const std::size_t ni = c->graph.inputs().size(), no = c->graph.outputs().size();
+    // The sets' pointers, built once: binding a set then only copies them in.
+    std::vector<std::vector<const void*>> ins(static_cast<std::size_t>(sets));
+    std::vector<std::vector<void*>> outs(static_cast<std::size_t>(sets));
+    for (int r = 0; r < sets; ++r) {
+        ins[r].assign(set_inputs + static_cast<std::size_t>(r) * ni, set_inputs + (static_cast<std::size_t>(r) + 1) * ni);
+        outs[r].assign(set_outputs + static_cast<std::size_t>(r) * no,
+                       set_outputs + (static_cast<std::size_t>(r) + 1) * no);
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < steps; ++i) {
+        if (sets > 0) {
+            const std::size_t r = static_cast<std::size_t>(i % sets);
+            Status st = c->exe->bind_inputs(ins[r]);
+            if (st.ok()) st = c->exe->bind_outputs(outs[r]);
+            if (!st.ok()) return fail("mc_enqueue_steps: " + st.message());
+        }
+        Status st = launch < 0 ? c->exe->enqueue(stream) : c->exe->enqueue_launch(static_cast<std::size_t>(launch), stream);
+        if (!st.ok()) return fail("mc_enqueue_steps: " + st.message());
+    }
+    if (host_us_per_step) {
+        const double us = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+        *host_us_per_step = steps > 0 ? us / steps : 0.0;
+    }
+    return 0;
+}
+
 MC_API int mc_download(void* h, float* const* outputs) {
     Compiled* c = as_compiled(h);
     if (!c->exe) return fail("mc_download: no executable");
@@ -457,7 +495,8 @@ MC_API int mc_gpu_device_json(const double* clocks, int n, char* out, int size) 
       << ",\"l2_bytes\":" << i.l2_bytes << ",\"lds_bytes_per_block\":" << i.lds_bytes_per_block
       << ",\"runtime_version\":" << i.runtime_version << ",\"driver_version\":" << i.driver_version
       << ",\"peak_bandwidth_gbs\":" << i.peak_bandwidth_gbs() << ",\"peak_fp32_gflops\":" << i.peak_fp32_gflops(i.clock_mhz)
-      << ",\"peak_bf16_gflops\":" << i.peak_bf16_gflops(i.clock_mhz) << ",\"clocks\":{\"samples\":" << count
+      << ",\"peak_bf16_gflops\":" << i.peak_bf16_gflops(i.clock_mhz)
+      << ",\"clock_now_mhz\":" << hip::current_clock_mhz(0) << ",\"clocks\":{\"samples\":" << count
       << ",\"min_mhz\":" << lo << ",\"max_mhz\":" << hi << ",\"mean_mhz\":" << mean << "}}";
     const std::string text = o.str();
     if (static_cast<int>(text.size()) >= size) return 2;
@@ -818,6 +857,11 @@ MC_API int mc_event_create(void** event) { return mchip_event_create(event); }
 MC_API int mc_event_destroy(void* event) { return mchip_event_destroy(event); }
 MC_API int mc_event_record(void* event, void* stream) { return mchip_event_record(event, stream); }
 MC_API int mc_event_elapsed_ms(void* start, void* stop, float* ms) { return mchip_event_elapsed_ms(ms, start, stop); }
+MC_API int mc_stream_begin_capture(void* stream) { return mchip_capture_begin(stream); }
+MC_API int mc_stream_end_capture(void* stream, void** graph_exec) { return mchip_capture_end(stream, graph_exec); }
+MC_API int mc_graph_launch(void* graph_exec, void* stream) { return mchip_graph_launch(graph_exec, stream); }
+MC_API int mc_graph_destroy(void* graph_exec) { return mchip_graph_exec_destroy(graph_exec); }
+
 MC_API const char* mc_error_string(int code) { return mchip_error_string(code); }
 
 }  // extern "C"

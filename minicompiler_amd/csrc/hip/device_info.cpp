@@ -1,5 +1,5 @@
-// Device queries (replaces the reference's src/cuda/device_info.cpp:33-73,
-// which read CUDA properties and NVML clocks).
+// Device queries (replaces the reference's src/cuda/device_info.cpp:33-66,
+// which read CUDA properties; the live clock is in engine_clock.cpp).
 
 #include "hip_rt.h"
 #include "minicompiler/hip/hip_backend.hpp"
@@ -30,11 +30,6 @@ Result<DeviceInfo> query_device(int device) {
     info.runtime_version = p.runtime_version;
     info.driver_version = p.driver_version;
     return info;
-}
-
-double current_clock_mhz(int device) {
-    int khz = 0;
-    return mchip_clock_khz_now(device, &khz) == 0 ? khz / 1000.0 : 0.0;
 }
 
 }  // namespace minicompiler::hip

@@ -47,11 +47,11 @@ int mchip_device_props(int device, mchip_props* out) {
 
 int mchip_set_device(int device) { return hipSetDevice(device); }
 
-int mchip_clock_khz_now(int device, int* khz) {
-    // The runtime reports the maximum engine clock; there is no query of the
-    // instantaneous clock in HIP itself.
+int mchip_clock_khz_max(int device, int* khz) {
     return hipDeviceGetAttribute(khz, hipDeviceAttributeClockRate, device);
 }
+
+int mchip_device_pci_bus_id(int device, char* out, int size) { return hipDeviceGetPCIBusId(out, size, device); }
 
 int mchip_malloc(void** ptr, size_t bytes) { return hipMalloc(ptr, bytes); }
 int mchip_free(void* ptr) { return hipFree(ptr); }

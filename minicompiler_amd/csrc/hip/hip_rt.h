@@ -38,7 +38,10 @@ const char* mchip_error_string(int code);
 int mchip_device_count(int* count);
 int mchip_device_props(int device, mchip_props* props);
 int mchip_set_device(int device);
-int mchip_clock_khz_now(int device, int* khz);
+/* The maximum engine clock the runtime reports (kHz). */
+int mchip_clock_khz_max(int device, int* khz);
+/* "dddd:bb:dd.f", the device's PCI address. */
+int mchip_device_pci_bus_id(int device, char* out, int size);
 
 int mchip_malloc(void** ptr, size_t bytes);
 int mchip_free(void* ptr);

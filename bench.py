@@ -424,26 +424,29 @@ def sample_rows(full: int, first: int, per_call, target_s: float = 0.25) -> int:
     return int(max(1, min(full, round(first * target_s / el))))
 
 
-def cpu_entry(per_row_work: float, unit: str, rows: int, full_rows: int, call, what: str,
+def cpu_entry(per_row_work: float, unit: str, rows: int, full_rows: int, cap_rows: int, call_of, what: str,
               seconds: float) -> dict:
-    """One and all-threads timings of call() (rows of the workload), as the
-    throughput of `per_row_work` units per row."""
+    """One-thread timing of call_of(rows)() and, on this GPU's host share,
+    of call_of(rows x threads)() (more rows, so every thread has a share of
+    the same size; at most cap_rows), as throughputs of `per_row_work` units
+    per row."""
     from oracle import oracle as orc
 
     out = {}
-    for threads, secs in ((1, seconds), (cpu_threads(), seconds / 2)):
-        orc.set_threads(threads)
-        per, reps = cpu_time(call, secs)
-        out[threads] = (per_row_work * rows / per / (1e12 if unit == "TFLOP/s" else 1e9), per, reps)
+    threads = cpu_threads()
+    for t, r, secs in ((1, rows, seconds), (threads, min(cap_rows, rows * threads), seconds / 2)):
+        orc.set_threads(t)
+        per, reps = cpu_time(call_of(r), secs)
+        out[t] = (per_row_work * r / per / (1e12 if unit == "TFLOP/s" else 1e9), per, reps, r)
     orc.set_threads(1)
-    v1, per1, reps1 = out[1]
-    va, pera, repsa = out[cpu_threads()]
+    v1, per1, reps1, _ = out[1]
+    va, pera, repsa, ra = out[threads]
     return {"value": v1, "unit": unit, "cores": 1, "threads": 1, "kind": "port",
             "sample": f"{what}: rows 0..{rows - 1} of {full_rows}, {reps1} calls, median {per1 * 1e3:.2f} ms/call, "
                       f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM; Eigen is not on the box), "
                       f"1 thread, {os.cpu_count()} host cores",
-            "all_cores": {"value": va, "threads": cpu_threads(),
-                          "sample": f"the same rows, {repsa} calls, median {pera * 1e3:.2f} ms/call"}}
+            "all_cores": {"value": va, "threads": threads,
+                          "sample": f"rows 0..{ra - 1}, {repsa} calls, median {pera * 1e3:.2f} ms/call"}}
 
 
 def cpu_baseline_graph(mc, name: str, dims_of, full_rows: int, row_elems: int, make_input, per_row_work: float,
@@ -456,22 +459,20 @@ def cpu_baseline_graph(mc, name: str, dims_of, full_rows: int, row_elems: int, m
 
     def prepared(rows):
         if rows not in cache:
+            cache.clear()
             c = mc.Compiled(path=mc.graph_path(name), dims=dims_of(rows), backend="none")
             g = c.graph()
             consts = {nd["id"]: c.constant(nd["id"]) for nd in g["nodes"] if nd["op_name"] == "const"}
-            cache.clear()
             cache[rows] = (g, consts, make_input(rows * row_elems))
         return cache[rows]
 
-    def run(rows):
+    def call_of(rows):
         g, consts, x = prepared(rows)
-        orc.evaluate(g, consts, [x])
+        return lambda: orc.evaluate(g, consts, [x])
 
     orc.set_threads(1)
-    prepared(first)
-    rows = sample_rows(full_rows, first, run)
-    prepared(rows)
-    return cpu_entry(per_row_work, unit, rows, full_rows, lambda: run(rows), f"{name} {dims_of(full_rows)}", seconds)
+    rows = sample_rows(full_rows, first, lambda r: call_of(r)())
+    return cpu_entry(per_row_work, unit, rows, full_rows, full_rows, call_of, f"{name} {dims_of(full_rows)}", seconds)
 
 
 def cpu_baseline_gemm(mc, m: int, n: int, k: int, seconds: float, what: str = "") -> dict:
@@ -481,12 +482,12 @@ def cpu_baseline_gemm(mc, m: int, n: int, k: int, seconds: float, what: str = ""
     from oracle import oracle as orc
 
     b = mc.uniform(k * n, 2, -1.0, 1.0)
-    a_full_rows = min(m, 4096)
-    a = mc.uniform(a_full_rows * k, 1, -1.0, 1.0)
+    a_rows = min(m, 2048)
+    a = mc.uniform(a_rows * k, 1, -1.0, 1.0)
     orc.set_threads(1)
-    run = lambda r: orc.matmul(a[:r * k], b, r, k, n)
-    rows = sample_rows(min(m, a_full_rows), min(m, 4), run)
-    return cpu_entry(2.0 * n * k, "TFLOP/s", rows, m, lambda: run(rows), what or f"fp32 gemm {m}x{n}x{k}", seconds)
+    call_of = lambda r: (lambda: orc.matmul(a[:r * k], b, r, k, n))
+    rows = sample_rows(a_rows, min(m, 4), lambda r: call_of(r)())
+    return cpu_entry(2.0 * n * k, "TFLOP/s", rows, m, a_rows, call_of, what or f"fp32 gemm {m}x{n}x{k}", seconds)
 
 
 def cpu_baseline(batch_rows: int, seconds: float) -> dict:

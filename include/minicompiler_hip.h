@@ -155,12 +155,15 @@ MC_API int mc_print_graph(const void* handle, char* out, int size);
 MC_API int mc_generate_elementwise_kernel(const char* program, const char* input_shapes, const char* out_shape,
                                           int allow_vectorize, int items_per_lane, int* vectorized, char* out,
                                           int size);
-/* The FP32 matrix-core GEMM whose store applies `program` (its input
+/* The matrix-core GEMM whose store applies `program` (its input
  * `acc_input` is the accumulated value; the others are read by access class
  * against `out_shape`), as the executable generates it for a matmul with a
- * fused elementwise consumer. Works without a device. */
+ * fused elementwise consumer, on GEMM body `body`: "two_stage" (or NULL),
+ * "ring_big", "ring_wide", "ring_mid", "ring_thin", "narrow16",
+ * "narrow32", "bf16", "f16". Works without a device. */
 MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
-                                            const char* out_shape, int vectorized_operands, char* out, int size);
+                                            const char* out_shape, int vectorized_operands, const char* body,
+                                            char* out, int size);
 /* hipRTC-compiles `source` for `arch` (e.g. "gfx950") to a code object with
  * the generator's options; no device needed. Returns 0 or 1; the log goes to
  * `log`. */

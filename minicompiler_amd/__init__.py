@@ -97,7 +97,7 @@ _SIGNATURES = {
     "mc_print_graph": (_i, [_vp, _cp, _i]),
     "mc_generate_elementwise_kernel": (_i, [_cp, _cp, _cp, _i, _i, _c.POINTER(_i), _cp, _i]),
     "mc_compile_kernel_source": (_i, [_cp, _cp, _cp, _i]),
-    "mc_generate_gemm_epilogue_kernel": (_i, [_cp, _i, _cp, _cp, _i, _cp, _i]),
+    "mc_generate_gemm_epilogue_kernel": (_i, [_cp, _i, _cp, _cp, _i, _cp, _cp, _i]),
     "mc_launch_matmul": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "mc_launch_matmul_cfg": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _i]),
     "mc_launch_matmul_lowp": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp]),
@@ -590,7 +590,7 @@ def noalloc_scratch_bytes() -> int:
     return int(library().mc_noalloc_scratch_bytes())
 
 
-RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4}
+RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4, "narrow": 5}
 
 
 def launch_matmul_cfg(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: int, stream=None,
@@ -662,10 +662,11 @@ def generate_elementwise_kernel(program: str, input_shapes: Sequence[Sequence[in
 
 
 def generate_gemm_epilogue_kernel(program: str, acc_input: int, input_shapes: Sequence[Sequence[int]],
-                                  out_shape: Sequence[int], vectorized_operands: bool = True) -> str:
+                                  out_shape: Sequence[int], vectorized_operands: bool = True,
+                                  body: str = "two_stage") -> str:
     shapes = ";".join("[" + ",".join(str(d) for d in s) + "]" for s in input_shapes)
     out = "[" + ",".join(str(d) for d in out_shape) + "]"
-    args = (program.encode(), acc_input, shapes.encode(), out.encode(), int(vectorized_operands))
+    args = (program.encode(), acc_input, shapes.encode(), out.encode(), int(vectorized_operands), body.encode())
     return _text_call(library().mc_generate_gemm_epilogue_kernel, *args)
 
 

@@ -128,12 +128,12 @@ Result<hip::HipOptions> parse_options(const char* spec) {
         } else if (key == "autotune") {
             o.autotune = value != "0" && value != "false";
         } else if (key == "ring") {
-            static const char* const names[] = {"auto", "wide", "mid", "big", "thin"};
+            static const char* const names[] = {"auto", "wide", "mid", "big", "thin", "narrow"};
             int cfg = -1;
-            for (int i = 0; i < 5; ++i) {
+            for (int i = 0; i < 6; ++i) {
                 if (value == names[i]) cfg = i;
             }
-            if (cfg < 0) return Error{"option ring=" + value + ": expected auto, wide, mid, big or thin"};
+            if (cfg < 0) return Error{"option ring=" + value + ": expected auto, wide, mid, big, thin or narrow"};
             o.ring_config = cfg;
         } else if (key == "ew_nt_loads") {
             o.nontemporal_loads = value != "0" && value != "false";
@@ -733,7 +733,30 @@ MC_API int mc_generate_elementwise_kernel(const char* program, const char* input
 }
 
 MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
-                                            const char* out_shape, int vectorized_operands, char* out, int size) {
+                                            const char* out_shape, int vectorized_operands, const char* body,
+                                            char* out, int size) {
+    struct BodyName {
+        const char* name;
+        hip::GemmBody body;
+        const char* const* source;
+    };
+    static const BodyName kBodies[] = {
+        {"two_stage", hip::GemmBody::F32Mfma, &hip::kGemmF32MfmaSource},
+        {"ring_big", hip::GemmBody::F32RingBig, &hip::kGemmF32RingSource},
+        {"ring_wide", hip::GemmBody::F32RingWide, &hip::kGemmF32RingSource},
+        {"ring_mid", hip::GemmBody::F32RingMid, &hip::kGemmF32RingSource},
+        {"ring_thin", hip::GemmBody::F32RingThin, &hip::kGemmF32RingSource},
+        {"narrow16", hip::GemmBody::F32Narrow16, &hip::kGemmF32NarrowSource},
+        {"narrow32", hip::GemmBody::F32Narrow32, &hip::kGemmF32NarrowSource},
+        {"bf16", hip::GemmBody::Bf16Fast, &hip::kGemm16FastSource},
+        {"f16", hip::GemmBody::F16Fast, &hip::kGemm16FastSource},
+    };
+    const BodyName* chosen = nullptr;
+    const std::string want = body && *body ? body : "two_stage";
+    for (const BodyName& b : kBodies) {
+        if (want == b.name) chosen = &b;
+    }
+    if (chosen == nullptr) return fail("mc_generate_gemm_epilogue_kernel: unknown body '" + want + "'"), -1;
     Result<FusedProgram> p = parse_program(program ? program : "");
     if (!p.ok()) return fail(p.error().message), -1;
     std::vector<Shape> shapes;
@@ -753,7 +776,7 @@ MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, 
     }
     const hip::GemmEpilogueKernel k = hip::generate_gemm_epilogue_kernel(
         p.value(), static_cast<std::size_t>(acc_input), shapes, os.value(), vectorized_operands != 0,
-        hip::kGemmF32MfmaSource);
+        *chosen->source, chosen->body);
     return copy_text(out, size, k.source);
 }
 

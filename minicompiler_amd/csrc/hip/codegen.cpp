@@ -207,8 +207,9 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
            << ">(a, b, c, " << mnk << ", epi);\n}\n";
         return {os.str()};
     }
-    const char* bounds =
-        body == GemmBody::F32RingBig || body == GemmBody::F32RingThin ? "256, 1" : "256, 2";
+    const char* bounds = body == GemmBody::F32RingBig || body == GemmBody::F32RingThin ? "256, 1"
+                         : is_narrow_body(body)                                        ? "256"
+                                                                                       : "256, 2";
     os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
           "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n"
@@ -216,6 +217,9 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
     if (body == GemmBody::F32Mfma) {
         os << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false") << ">(a, b, c, " << mnk
            << ", " << (constant ? std::to_string(fixed.k_split) : std::string("k_split")) << ", partial, epi);\n}\n\n";
+    } else if (is_narrow_body(body)) {
+        os << "\tmc_gemm_f32_narrow<" << (body == GemmBody::F32Narrow16 ? "McNarrow16" : "McNarrow32") << ">(a, b, c, "
+           << mnk << ", " << split << ", partial, epi);\n}\n\n";
     } else {
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"
                           : body == GemmBody::F32RingThin ? "McRingThin"

@@ -77,13 +77,20 @@ enum class GemmBody {
     F32RingWide,  // likewise, 128x128 tiles, 2 stages, up to two blocks per CU
     F32RingThin,  // likewise, 32x128 tiles (M <= 32, or when the autotuner picks it), 6 stages
     F32RingMid,   // likewise, 64x128 tiles, 3 stages, up to two blocks per CU (autotuner only)
+    F32Narrow16,  // fp32 operands, 16x64 tiles on 16x16x4 MFMAs, K split over waves (gemm_f32_narrow.h), M <= 16
+    F32Narrow32,  // likewise, 32x64 tiles (split_k products with at most one tile per CU)
     Bf16Fast,     // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
     F16Fast,      // fp16 operands, likewise
 };
 
 inline bool is_f32_body(GemmBody body) {
     return body == GemmBody::F32Mfma || body == GemmBody::F32RingBig || body == GemmBody::F32RingWide ||
-           body == GemmBody::F32RingThin || body == GemmBody::F32RingMid;
+           body == GemmBody::F32RingThin || body == GemmBody::F32RingMid || body == GemmBody::F32Narrow16 ||
+           body == GemmBody::F32Narrow32;
+}
+
+inline bool is_narrow_body(GemmBody body) {
+    return body == GemmBody::F32Narrow16 || body == GemmBody::F32Narrow32;
 }
 
 // A GEMM (the matrix-core body in `gemm_body_source`, of kind `body`) whose

@@ -493,8 +493,11 @@ private:
                          "): gfx950 has bf16 and fp16 matrix instructions but no xf32 (TF32) one"};
         }
         l->splits = uses_split_k(l->matmul) ? matmul_splits(l->matmul, l->m, l->n, l->k, device_.cu_count) : 1;
-        if ((l->matmul == MatmulKernel::DoubleBuffered || l->matmul == MatmulKernel::SplitK) && l->k % 32 == 0 &&
-            l->n % 4 == 0) {
+        if (options_.ring_config == MCHIP_RING_NARROW) {
+            // The narrow-tile body: split_k only, K a multiple of 16.
+            if (l->matmul == MatmulKernel::SplitK && l->k % 16 == 0 && l->n % 4 == 0) l->ring_cfg = MCHIP_RING_NARROW;
+        } else if ((l->matmul == MatmulKernel::DoubleBuffered || l->matmul == MatmulKernel::SplitK) &&
+                   l->k % 32 == 0 && l->n % 4 == 0) {
             l->ring_cfg = options_.ring_config;  // a shape the ring cannot take keeps the planner's body
         }
         if (options_.autotune && options_.matmul == MatmulKernel::Auto) {
@@ -523,6 +526,16 @@ private:
     // 16-byte aligned).
     GemmBody fused_body(Launch& l) const {
         if (l.lowp) return l.dtype == MCHIP_DTYPE_BF16 ? GemmBody::Bf16Fast : GemmBody::F16Fast;
+        if (l.matmul == MatmulKernel::SplitK &&
+            (l.ring_cfg == MCHIP_RING_NONE || l.ring_cfg == MCHIP_RING_NARROW)) {
+            int rows = 0, splits = 0, k_split = 0;
+            if (mchip_f32_narrow_plan(l.m, l.n, l.k, std::max(l.splits, 1), device_.cu_count,
+                                      l.ring_cfg == MCHIP_RING_NARROW, &rows, &splits, &k_split)) {
+                l.k_split = k_split;
+                l.depth = splits;
+                return rows == 16 ? GemmBody::F32Narrow16 : GemmBody::F32Narrow32;
+            }
+        }
         split_layout(l.k, l.splits, &l.k_split, &l.depth);
         if (l.matmul == MatmulKernel::Vectorized || l.k % 4 != 0) return GemmBody::F32Mfma;
         unsigned grid = 0, block = 0;
@@ -603,6 +616,7 @@ private:
                 const GemmBody body = l.body;
                 const char* body_source = l.lowp                        ? kGemm16FastSource
                                           : body == GemmBody::F32Mfma ? kGemmF32MfmaSource
+                                          : is_narrow_body(body)      ? kGemmF32NarrowSource
                                                                       : kGemmF32RingSource;
                 GemmDims dims;
                 dims.m = l.m;
@@ -667,6 +681,12 @@ private:
                     l.grid_x = static_cast<unsigned>((l.n + 127) / 128);
                     l.grid_y = static_cast<unsigned>((l.m + 127) / 128);
                     l.grid_z = static_cast<unsigned>(l.depth);
+                    l.block = 256;
+                } else if (is_narrow_body(l.body)) {
+                    const int rows = l.body == GemmBody::F32Narrow16 ? 16 : 32;
+                    l.grid_x = static_cast<unsigned>((l.n + 63) / 64);
+                    l.grid_y = static_cast<unsigned>(l.depth);
+                    l.grid_z = static_cast<unsigned>((l.m + rows - 1) / rows);
                     l.block = 256;
                 } else {
                     unsigned grid = 0, block = 0;

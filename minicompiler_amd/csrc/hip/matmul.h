@@ -58,12 +58,38 @@ int mchip_matmul_blocks_per_cu(int kernel);
  *                    here, only when forced (the autotuner times it).
  * mchip_f32_ring_plan_cfg with cfg != MCHIP_RING_NONE forces that
  * configuration (thin then at any m), if the shape fits the ring at all. */
-enum { MCHIP_RING_NONE = 0, MCHIP_RING_WIDE = 1, MCHIP_RING_MID = 2, MCHIP_RING_BIG = 3, MCHIP_RING_THIN = 4 };
+enum {
+    MCHIP_RING_NONE = 0,
+    MCHIP_RING_WIDE = 1,
+    MCHIP_RING_MID = 2,
+    MCHIP_RING_BIG = 3,
+    MCHIP_RING_THIN = 4,
+    MCHIP_RING_NARROW = 5
+};
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);
 
+/* The narrow-tile body (gemm_f32_narrow.h), which the split_k rung runs for
+ * products whose 32x64 tiles (16x64 for m <= 16) number at most one per CU:
+ * K is cut into *splits ranges of *k_split (a multiple of 16), at most
+ * max_splits of them, so that tiles x ranges stays within the CUs. Its
+ * accumulation order is its own (16x16x4 MFMAs, K pieces per wave added
+ * in wave order, then the ranges in range order), not the ring body's.
+ * Returns 1 and fills *rows (16 or 32), *splits and *k_split when the plan
+ * runs the product on it (force: whenever the shape fits: k a multiple of
+ * 16, n of 4), else 0. */
+int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* rows, int* splits,
+                          int* k_split);
+
+/* The narrow-tile body directly: `rows` 16 (m <= 16) or 32, K in `splits`
+ * ranges; above one range the partials go to `workspace` (splits * m * n
+ * floats) and are summed in range order. */
+int mchip_launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, void* stream, int splits,
+                        int rows, float* workspace);
+
 /* mchip_launch_matmul with the ring configuration forced (MCHIP_RING_NONE:
- * the plan's own) for double_buffered and split_k; hipErrorInvalidValue
+ * the plan's own) for double_buffered and split_k (MCHIP_RING_NARROW: the
+ * narrow-tile body, split_k only); hipErrorInvalidValue
  * when that configuration cannot run the product (K not a multiple of 32, N
  * not of 4, operands not 16-byte aligned) or for other kernels. */
 int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,

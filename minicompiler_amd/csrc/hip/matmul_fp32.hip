@@ -26,6 +26,7 @@
 
 #include "gemm_f32_mfma.h"
 #include "gemm_f32_ring.h"
+#include "gemm_f32_narrow.h"
 
 #include <algorithm>
 #include <atomic>
@@ -168,6 +169,20 @@ __global__ void __launch_bounds__(Cfg::kThreads, kBlocksPerCu)
     mc_gemm_f32_ring<Cfg>(a, b, c, m, n, k, k_split, depth, partial, McGemmStore{});
 }
 
+// ---------------------------------------------------------------- narrow tiles
+
+struct McIdentity {
+    __device__ __forceinline__ float operator()(float v, unsigned) const { return v; }
+};
+
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::kThreads) matmul_narrow_f32(const float* __restrict__ a,
+                                                                    const float* __restrict__ b, float* __restrict__ c,
+                                                                    int m, int n, int k, int k_split, int depth,
+                                                                    float* __restrict__ partial) {
+    mc_gemm_f32_narrow<Cfg>(a, b, c, m, n, k, k_split, depth, partial, McIdentity{});
+}
+
 // ---------------------------------------------------------------- split-K sum
 
 // c[i] = partial[0][i] + partial[1][i] + ... in split order (a left fold,
@@ -221,8 +236,39 @@ int device_cu_count() {
     return cus;
 }
 
+// The narrow-tile body on `depth` K ranges of k_split, the partials summed
+// in range order when there are several.
+int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int rows,
+                  int k_split, int depth, float* workspace) {
+    float* dst = depth > 1 ? workspace : c;
+    if (!aligned16(a) || !aligned16(b) || dst == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((n + 63) / 64, depth, (m + rows - 1) / rows);
+    float* part = depth > 1 ? workspace : nullptr;
+    if (rows == 16) {
+        hipLaunchKernelGGL((matmul_narrow_f32<McNarrow16>), grid, dim3(McNarrow16::kThreads), 0, s, a, b, c, m, n, k,
+                           k_split, depth, part);
+    } else {
+        hipLaunchKernelGGL((matmul_narrow_f32<McNarrow32>), grid, dim3(McNarrow32::kThreads), 0, s, a, b, c, m, n, k,
+                           k_split, depth, part);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || depth == 1) return e;
+    return mchip_sum_split_partials(workspace, c, static_cast<std::size_t>(m) * n, depth, s);
+}
+
 int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
-                    hipStream_t stream, int splits, float* workspace, int ring_cfg) {
+                    hipStream_t stream, int splits, float* workspace, int ring_cfg, bool split_k) {
+    // split_k on the narrow-tile body when the plan (or the caller) takes it,
+    // with at most the caller's split count (its workspace's size).
+    if (split_k && (ring_cfg == MCHIP_RING_NONE || ring_cfg == MCHIP_RING_NARROW) && aligned16(a) && aligned16(b)) {
+        int rows = 0, ns = 0, nk = 0;
+        if (mchip_f32_narrow_plan(m, n, k, std::max(splits, 1), device_cu_count(), ring_cfg == MCHIP_RING_NARROW,
+                                  &rows, &ns, &nk)) {
+            if (ns > 1 && workspace == nullptr) return hipErrorInvalidValue;  // as the ring would
+            return launch_narrow(a, b, c, m, n, k, stream, rows, nk, ns, workspace);
+        }
+    }
+    if (ring_cfg == MCHIP_RING_NARROW) return hipErrorInvalidValue;
     const int k_split = split_len(k, splits, kMBK);
     const int depth = std::max(1, (k + k_split - 1) / k_split);
     if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
@@ -325,6 +371,40 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     return mchip_f32_ring_plan_cfg(m, n, k, depth, cu_count, MCHIP_RING_NONE, grid, block);
 }
 
+extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* rows,
+                                     int* splits, int* k_split) {
+    *rows = *splits = *k_split = 0;
+    if (m < 1 || n < 4 || n % 4 != 0 || k < 16 || k % 16 != 0 || max_splits < 1 || cu_count < 1) return 0;
+    const int r = m <= 16 ? 16 : 32;
+    const long long tiles = static_cast<long long>((m + r - 1) / r) * ((n + 63) / 64);
+    // Measured on an MI355X (one-matmul launches, operands past the MALL):
+    // against the ring body, the narrow body wins while its tiles fit one
+    // per CU (256x2048x512: 9.4 against 16.2 us; 256x512x2048 in 4 ranges
+    // 13.0 against 16.4; 512^3 8.9 against 13.0; 1024x512x2048 25.9 against
+    // 28.1; 16x4096x4096 in 4 ranges 17.2 against 20.6) and loses beyond
+    // (1024^3 34.8 against 28.1; 1024x2048x512 33.7 against 28.8): its
+    // tiles reuse each operand byte a third as often.
+    if (!force && tiles > cu_count) return 0;
+    // K ranges: the largest power of two that keeps tiles x ranges within
+    // the CUs and each range at least 64 deep.
+    int s = 1;
+    while (s * 2 <= max_splits && tiles * s * 2 <= cu_count && k / (s * 2) >= 64) s *= 2;
+    const int ks = ((k + s - 1) / s + 15) / 16 * 16;
+    *rows = r;
+    *k_split = ks;
+    *splits = (k + ks - 1) / ks;
+    return 1;
+}
+
+extern "C" int mchip_launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, void* stream,
+                                   int splits, int rows, float* workspace) {
+    if (m < 1 || n < 4 || n % 4 != 0 || k < 16 || k % 16 != 0 || splits < 1) return hipErrorInvalidValue;
+    if ((rows != 16 && rows != 32) || (rows == 16 && m > 16)) return hipErrorInvalidValue;
+    const int k_split = ((k + splits - 1) / splits + 15) / 16 * 16;
+    return launch_narrow(a, b, c, m, n, k, static_cast<hipStream_t>(stream), rows, k_split, (k + k_split - 1) / k_split,
+                         workspace);
+}
+
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
     if (splits < 1) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -385,9 +465,9 @@ extern "C" int mchip_launch_matmul(int kernel, const float* a, const float* b, f
             hipLaunchKernelGGL((matmul_register_tiled<64, 64, 8, 4, 4>), grid, dim3(256), 0, s, a, b, c, m, n, k);
             return hipGetLastError();
         }
-        case kVectorized: return launch_mfma_f32(false, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE);
-        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE);
-        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, MCHIP_RING_NONE);
+        case kVectorized: return launch_mfma_f32(false, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE, false);
+        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, MCHIP_RING_NONE, false);
+        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, MCHIP_RING_NONE, true);
         case kTensorCoreTf32:
         case kTensorCoreBf16:
         case kTensorCoreF16: return mchip_launch_tensor_core(kernel, a, b, c, m, n, k, stream, splits, workspace);
@@ -401,8 +481,10 @@ extern "C" int mchip_launch_matmul_cfg(int kernel, const float* a, const float* 
     if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (kernel) {
-        case kDoubleBuffered: return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, ring_cfg);
-        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, ring_cfg);
+        case kDoubleBuffered:
+            if (ring_cfg == MCHIP_RING_NARROW) return hipErrorInvalidValue;  // split_k only
+            return launch_mfma_f32(true, a, b, c, m, n, k, s, 1, nullptr, ring_cfg, false);
+        case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, ring_cfg, true);
         default: return hipErrorInvalidValue;  // only the ring rungs take a configuration
     }
 }

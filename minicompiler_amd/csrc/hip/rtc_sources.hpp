@@ -10,6 +10,9 @@ extern const char* const kGemmF32MfmaSource;
 // gemm_f32_ring.h: the FP32 matrix-core GEMM body with an LDS ring and
 // persistent blocks, with an epilogue hook (the same arithmetic).
 extern const char* const kGemmF32RingSource;
+// gemm_f32_narrow.h: the FP32 narrow-tile GEMM body (16x16x4 MFMAs, no
+// LDS staging) with an epilogue hook.
+extern const char* const kGemmF32NarrowSource;
 // gemm_mfma16_fast.h: the bf16 / fp16 matrix-core GEMM body (16-bit inputs
 // in HBM) with an epilogue hook.
 extern const char* const kGemm16FastSource;

@@ -124,6 +124,25 @@ def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, ou
     assert ok, log
 
 
+@pytest.mark.parametrize("body,call", [("ring_big", "mc_gemm_f32_ring<McRingBig>"),
+                                       ("ring_wide", "mc_gemm_f32_ring<McRingWide>"),
+                                       ("ring_thin", "mc_gemm_f32_ring<McRingThin>"),
+                                       ("ring_mid", "mc_gemm_f32_ring<McRingMid>"),
+                                       ("narrow16", "mc_gemm_f32_narrow<McNarrow16>"),
+                                       ("narrow32", "mc_gemm_f32_narrow<McNarrow32>"),
+                                       ("bf16", "mc_gemm16_fast<true>"), ("f16", "mc_gemm16_fast<false>")])
+def test_every_gemm_body_with_an_epilogue_compiles_for_gfx950(mc, body, call):
+    # bias + tanh on the product, as a fused group reads it: each GEMM body the
+    # executable can pick, compiled by hipRTC with no device.
+    text = "r0 = load in0\nr1 = load in1\nr2 = add r0, r1\nr3 = tanh r2\n"
+    src = mc.generate_gemm_epilogue_kernel(text, 0, [(96, 256), (256,)], (96, 256), True, body)
+    assert call in src
+    ok, log = mc.compile_kernel_source(src, "gfx950")
+    assert ok, log
+    with pytest.raises(mc.MinicompilerError, match="unknown body"):
+        mc.generate_gemm_epilogue_kernel(text, 0, [(96, 256), (256,)], (96, 256), True, "tiny")
+
+
 def test_a_bad_generated_source_returns_the_hiprtc_log(mc):
     ok, log = mc.compile_kernel_source('extern "C" __global__ void mc_elementwise() { undefined_thing(); }')
     assert not ok and "undefined_thing" in log and "hipRTC could not compile" in log

@@ -322,6 +322,22 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
             e["frac_hbm"] = e["gbs"] / PEAK_HBM_GBS
         n_sets = len(sets)
         del sets, launches
+        # The same product as a one-matmul compiled graph (the library's own
+        # path: mcc, the C ABI's mc_compile): narrow-tile split_k products
+        # add their K ranges inside the GEMM kernel there.
+        gg = mc.Compiled(f"graph gemm\ninput a : f32[{m}, {k}]\ninput b : f32[{k}, {n}]\nc = matmul a, b\n"
+                         f"output c\n")
+        rot, bufs = graph_rotation(mc, gg, lambda: [a_host, b_host])
+        tg = time_graph(mc, gg, steps, warmup, rot, warm_seconds=WARM_SECONDS)
+        gms = tg["launch_ms"][0]
+        e["graph"] = {"ms": gms, "ms_range": tg["launch_ms_range"][0], "launch": gg.launch_names[0],
+                      "tflops": flop / (gms * 1e-3) / 1e12, "buffer_sets": len(rot)}
+        if m <= 32:
+            e["graph"]["gbs"] = e["bytes"] / (gms * 1e-3) / 1e9
+        gg.close()
+        del bufs
+        log(f"gemm fp32 {m}x{n}x{k} compiled graph ({e['graph']['launch']}): {gms:.4f} ms "
+            f"{e['graph']['tflops']:.1f} TFLOP/s")
         if splits > 1 or m <= 32:
             # The same product as a one-matmul graph compiled with autotune=1
             # (split count and tile configuration timed at compile time).
@@ -518,25 +534,55 @@ FP32_SHAPES = [(1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096), (8192
 LOWP_SHAPES = [(8192, 8192, 8192), (4096, 14336, 4096)]
 
 
-def run_configs(mc, args, cus: int, line: dict, cpu_s: float) -> None:
-    """BASELINE's other configs, each with its CPU baseline (cpu_s seconds
-    of one-thread CPU work, half that on all threads; 0: none)."""
+def cpu_baselines(mc, args, cpu_s: float, headline_s: float) -> dict:
+    """Every CPU baseline, computed before any GPU timing (the GPU idles
+    meanwhile and drops its clock, so this work must not sit between the GPU
+    configs and the headline). Keys: config names, ("gemm", m, n, k) and
+    ("epilogue", m, n, k); "headline" for the MLP. cpu_s: seconds of
+    one-thread work per config (half that on all threads), 0 for none."""
+    out = {}
+    if cpu_s <= 0:
+        return out
+    want = lambda w: args.workload == w or (args.workload == "mlp" and not args.quick)
+    if want("gelu"):
+        out["gelu"] = cpu_baseline_graph(mc, "gelu_chain", lambda r: {"M": r, "N": 4096}, 4096, 4096,
+                                         lambda n: mc.uniform(n, 1, -3.0, 3.0), 8.0 * 4096, "GB/s", 16, cpu_s)
+    if want("batchnorm"):
+        out["batchnorm"] = cpu_baseline_graph(mc, "batchnorm_relu", lambda r: {"R": r, "C": 256}, 200704, 256,
+                                              lambda n: mc.normal(n, 1, 0.0, 1.0), 8.0 * 256, "GB/s", 256, cpu_s)
+    shapes = set()
+    if want("gemm_fp32"):
+        shapes |= set(FP32_SHAPES)
+    if want("gemm_bf16"):
+        shapes |= set(LOWP_SHAPES)
+    for m, n, k in sorted(shapes):
+        out[("gemm", m, n, k)] = cpu_baseline_gemm(mc, m, n, k, cpu_s)
+    if want("gemm_bf16"):
+        for m, n, k in LOWP_SHAPES:
+            out[("epilogue", m, n, k)] = cpu_baseline_graph(
+                mc, "matmul_bias_gelu", lambda r, k=k, n=n: {"M": r, "K": k, "N": n}, m, k,
+                lambda cnt: mc.uniform(cnt, 1, -1.0, 1.0), 2.0 * n * k, "TFLOP/s", 2, cpu_s)
+    if args.workload == "mlp" and headline_s > 0:
+        out["headline"] = cpu_baseline(256, headline_s)
+    return out
+
+
+def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
+    """BASELINE's other configs, each with its CPU baseline from `cpu`."""
     cfgs = line.setdefault("configs", {})
     want = lambda w: args.workload == w or (args.workload == "mlp" and not args.quick)
     if want("gelu"):
         e = bench_elementwise_graph(mc, "gelu_chain", {"M": 4096, "N": 4096}, lambda n: mc.uniform(n, 1, -3.0, 3.0),
                                     args.steps, args.warmup)
-        if cpu_s:
-            e["cpu_baseline"] = cpu_baseline_graph(mc, "gelu_chain", lambda r: {"M": r, "N": 4096}, 4096, 4096,
-                                                   lambda n: mc.uniform(n, 1, -3.0, 3.0), 8.0 * 4096, "GB/s", 16, cpu_s)
+        if "gelu" in cpu:
+            e["cpu_baseline"] = cpu["gelu"]
         cfgs["gelu_4096x4096"] = e
         log(f"gelu: {e['gbs']:.0f} GB/s, host {e['host_us_per_step']:.1f} us/step")
     if want("batchnorm"):
         e = bench_elementwise_graph(mc, "batchnorm_relu", {"R": 200704, "C": 256},
                                     lambda n: mc.normal(n, 1, 0.0, 1.0), args.steps, args.warmup)
-        if cpu_s:
-            e["cpu_baseline"] = cpu_baseline_graph(mc, "batchnorm_relu", lambda r: {"R": r, "C": 256}, 200704, 256,
-                                                   lambda n: mc.normal(n, 1, 0.0, 1.0), 8.0 * 256, "GB/s", 256, cpu_s)
+        if "batchnorm" in cpu:
+            e["cpu_baseline"] = cpu["batchnorm"]
         cfgs["batchnorm_relu_200704x256"] = e
         log(f"batchnorm: {e['gbs']:.0f} GB/s, host {e['host_us_per_step']:.1f} us/step")
     if args.workload == "mlp" and not args.quick:
@@ -553,38 +599,31 @@ def run_configs(mc, args, cus: int, line: dict, cpu_s: float) -> None:
                                "host_us_per_step": r["timing"]["host_us_per_step"],
                                "launch_ms": r["timing"]["launch_ms"]}
                 del r
-            entry["cpu_baseline"] = "the headline's cpu_baseline (mlp_gelu rows; rows are independent)"
+            if "headline" in cpu:
+                entry["cpu_baseline"] = cpu["headline"]
             cfgs[f"mlp_b{b}"] = entry
             log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
                 f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step, "
                 f"autotuned {entry['autotuned']['ms_per_step'] * 1e3:.1f} us/step")
-    cpu_gemm = {}
     if want("gemm_fp32"):
         g = bench_gemm_fp32(mc, cus, FP32_SHAPES, 20, 2)  # plus WARM_SECONDS per shape
         for e in g:
-            if cpu_s:
-                key = (e["m"], e["n"], e["k"])
-                cpu_gemm[key] = e["cpu_baseline"] = cpu_baseline_gemm(mc, *key, cpu_s)
+            key = ("gemm", e["m"], e["n"], e["k"])
+            if key in cpu:
+                e["cpu_baseline"] = cpu[key]
         cfgs["gemm_fp32"] = g
     if want("gemm_bf16"):
         g = bench_gemm_lowp(mc, LOWP_SHAPES, 20, 2)  # plus WARM_SECONDS
         for e in g:
-            if cpu_s:
-                key = (e["m"], e["n"], e["k"])
-                if key not in cpu_gemm:
-                    cpu_gemm[key] = cpu_baseline_gemm(mc, *key, cpu_s)
-                e["cpu_baseline"] = cpu_gemm[key]
+            key = ("gemm", e["m"], e["n"], e["k"])
+            if key in cpu:
+                e["cpu_baseline"] = cpu[key]
         cfgs["gemm_bf16_fp16"] = g
         ep = bench_lowp_epilogue(mc, LOWP_SHAPES, 20, 2)
-        cpu_ep = {}
         for e in ep:
-            if cpu_s:
-                m, n, k = e["m"], e["n"], e["k"]
-                if (m, n, k) not in cpu_ep:
-                    cpu_ep[(m, n, k)] = cpu_baseline_graph(
-                        mc, "matmul_bias_gelu", lambda r, k=k, n=n: {"M": r, "K": k, "N": n}, m, k,
-                        lambda cnt: mc.uniform(cnt, 1, -1.0, 1.0), 2.0 * n * k, "TFLOP/s", 2, cpu_s)
-                e["cpu_baseline"] = cpu_ep[(m, n, k)]
+            key = ("epilogue", e["m"], e["n"], e["k"])
+            if key in cpu:
+                e["cpu_baseline"] = cpu[key]
         cfgs["gemm_bf16_fp16_bias_gelu"] = ep
 
 
@@ -619,9 +658,11 @@ def main() -> int:
             "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded splitmix64 uniform/normal, "
                                                             "random-init constants of the graph)"}
     cpu_s = 0.0 if args.no_cpu_baseline else args.config_cpu_seconds
+    cpu = cpu_baselines(mc, args, cpu_s, 0.0 if args.no_cpu_baseline else args.cpu_seconds)
+    log(f"cpu baselines: {len(cpu)} workloads")
     whole = ClockSampler(mc, period_s=0.05)
     with whole:
-        run_configs(mc, args, cus, line, cpu_s)
+        run_configs(mc, args, cus, line, cpu)
     cfgs = line.get("configs", {})
     sampler = ClockSampler(mc)
 
@@ -682,10 +723,10 @@ def main() -> int:
     line["device"] = {k: d[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
     line["device"]["clocks"] = {**d["clocks"], "during": "the headline's timed steps",
                                 "source": "AMD SMI current GFX clock (mean over XCDs), sampled every 2 ms"}
-    line["device"]["clocks_configs"] = {**whole.summary(), "during": "the other configs (GPU and CPU work)",
+    line["device"]["clocks_configs"] = {**whole.summary(), "during": "the other configs' GPU work",
                                         "period_ms": 50}
-    if not args.no_cpu_baseline and args.workload == "mlp":
-        line["cpu_baseline"] = cpu_baseline(256, args.cpu_seconds)
+    if "headline" in cpu:
+        line["cpu_baseline"] = cpu["headline"]
     print(json.dumps(line), flush=True)
     return 0
 

@@ -683,10 +683,10 @@ private:
                     l.grid_z = static_cast<unsigned>(l.depth);
                     l.block = 256;
                 } else if (is_narrow_body(l.body)) {
+                    // One-dimensional: the body maps blocks to tiles XCD by XCD.
                     const int rows = l.body == GemmBody::F32Narrow16 ? 16 : 32;
-                    l.grid_x = static_cast<unsigned>((l.n + 63) / 64);
-                    l.grid_y = static_cast<unsigned>(l.depth);
-                    l.grid_z = static_cast<unsigned>((l.m + rows - 1) / rows);
+                    l.grid_x = static_cast<unsigned>(((l.n + 63) / 64) * l.depth * ((l.m + rows - 1) / rows));
+                    l.grid_y = l.grid_z = 1;
                     l.block = 256;
                 } else {
                     unsigned grid = 0, block = 0;

@@ -242,12 +242,13 @@ int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k,
                   int k_split, int depth, float* workspace) {
     float* dst = depth > 1 ? workspace : c;
     if (!aligned16(a) || !aligned16(b) || dst == nullptr) return hipErrorInvalidValue;
-    const dim3 grid((n + 63) / 64, depth, (m + rows - 1) / rows);
     float* part = depth > 1 ? workspace : nullptr;
     if (rows == 16) {
+        const dim3 grid(((n + McNarrow16::kCols - 1) / McNarrow16::kCols) * depth * ((m + 15) / 16));
         hipLaunchKernelGGL((matmul_narrow_f32<McNarrow16>), grid, dim3(McNarrow16::kThreads), 0, s, a, b, c, m, n, k,
                            k_split, depth, part);
     } else {
+        const dim3 grid(((n + McNarrow32::kCols - 1) / McNarrow32::kCols) * depth * ((m + 31) / 32));
         hipLaunchKernelGGL((matmul_narrow_f32<McNarrow32>), grid, dim3(McNarrow32::kThreads), 0, s, a, b, c, m, n, k,
                            k_split, depth, part);
     }

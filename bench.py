@@ -8,13 +8,15 @@ pass over one batch of synthetic, seeded input already resident in HBM).
 The headline workload is BASELINE config 2, the fp32 MLP block
 (mlp_gelu.mcg) at B=8192: GEMM with bias+GELU fused into its store, GEMM
 with bias+residual fused into its store. The other configurations run
-first (each after WARM_SECONDS of its own work), so the headline's W
-untimed steps and K timed steps find the GPU at its working clock; the K
-steps are timed between two HIP events on the executable's stream and are
-issued by one library call (mc_enqueue_steps), so no per-step Python work
-sits in the timed region. Each kernel's duration is then measured in the
-same process on the same stream: the launch alone, back to back, between
-one pair of HIP events. GEMM operator rows are timed from a captured HIP
+first (each after WARM_SECONDS of its own work). The headline then times
+each of its launches alone (after WARM_SECONDS of its own steps; back to
+back between one pair of HIP events on the executable's stream), then runs
+W untimed steps and K timed steps: the K steps find the GPU at the clock it
+holds under this work, whatever W is (it idles while the graph compiles and
+its buffers upload, and takes 30-40 ms of work to come back). The K steps
+are timed between two HIP events on the executable's stream and are issued
+by one library call (mc_enqueue_steps), so no per-step Python work sits in
+the timed region. GEMM operator rows are timed from a captured HIP
 graph of back-to-back launches over rotating operand sets (no host launch
 cost; the reference times its GEMMs from a graph, bench_cuda.cpp:445-493).
 Every configuration rotates over buffer sets whose footprint exceeds twice
@@ -156,7 +158,7 @@ def rotation_sets(set_bytes: int) -> int:
 
 
 def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None,
-               warm_seconds: float = 0.0, sampler: ClockSampler | None = None) -> dict:
+               warm_seconds: float = 0.0, sampler: ClockSampler | None = None, launches_first: bool = False) -> dict:
     """W warmup steps (then more until `warm_seconds` have passed), then K
     steps timed between one pair of HIP events on the executable's stream
     (ms_per_step); the K steps are one mc_enqueue_steps call, whose host time
@@ -165,17 +167,44 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     mean duration, with no event between launches to perturb it), in RUNS
     runs: the median run, and the range. `rotations`: list of (input_ptrs,
     output_ptrs) bound in turn, so consecutive launches touch different
-    buffers (defeats the 256 MB MALL). `sampler` runs during the K steps."""
+    buffers (defeats the 256 MB MALL). `sampler` runs during the K steps.
+
+    launches_first: the per-launch timings (after `warm_seconds` of steps)
+    come before the W warmup steps and the K timed steps instead of after
+    them, so the timed steps run at the clock the GPU holds under this work
+    whatever W is (an MI355X takes 30-40 ms of back-to-back work to reach
+    it from idle, and idles while the graph is compiled and its buffers are
+    uploaded)."""
     stream = compiled.stream
-    compiled.enqueue_steps(warmup, sets=rotations)
-    compiled.synchronize()
+    start, stop = mc.Event(), mc.Event()
+    reps = reps or max(steps, 10)
 
     def extra():
         compiled.enqueue_steps(max(warmup, 10), sets=rotations)
         compiled.synchronize()
 
-    warm_up_for(warm_seconds, extra)
-    start, stop = mc.Event(), mc.Event()
+    def per_launch():
+        launch_ms, launch_range = [], []
+        for j in range(compiled.kernel_launches):
+            compiled.enqueue_steps(2, launch=j, sets=rotations)
+            runs = []
+            for _ in range(RUNS):
+                start.record(stream)
+                compiled.enqueue_steps(reps, launch=j, sets=rotations)
+                stop.record(stream)
+                compiled.synchronize()
+                runs.append(start.elapsed_ms(stop) / reps)
+            launch_ms.append(statistics.median(runs))
+            launch_range.append([min(runs), max(runs)])
+        return launch_ms, launch_range
+
+    if launches_first:
+        warm_up_for(warm_seconds, extra)
+        launch_ms, launch_range = per_launch()
+    compiled.enqueue_steps(warmup, sets=rotations)
+    compiled.synchronize()
+    if not launches_first:
+        warm_up_for(warm_seconds, extra)
     if sampler is not None:
         sampler.__enter__()
     t0 = time.perf_counter()
@@ -187,21 +216,12 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     if sampler is not None:
         sampler.__exit__()
     total_ms = start.elapsed_ms(stop)
-    reps = reps or max(steps, 10)
-    launch_ms, launch_range = [], []
-    for j in range(compiled.kernel_launches):
-        compiled.enqueue_steps(2, launch=j, sets=rotations)
-        runs = []
-        for _ in range(RUNS):
-            start.record(stream)
-            compiled.enqueue_steps(reps, launch=j, sets=rotations)
-            stop.record(stream)
-            compiled.synchronize()
-            runs.append(start.elapsed_ms(stop) / reps)
-        launch_ms.append(statistics.median(runs))
-        launch_range.append([min(runs), max(runs)])
+    if not launches_first:
+        launch_ms, launch_range = per_launch()
     return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "host_us_per_step": host_us,
-            "launch_ms": launch_ms, "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS}
+            "launch_ms": launch_ms, "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS,
+            "order": "per-launch timings, then warmup and timed steps" if launches_first else
+                     "warmup and timed steps, then per-launch timings"}
 
 
 def graph_rotation(mc, compiled, make_inputs) -> tuple[list, list]:
@@ -220,13 +240,14 @@ def graph_rotation(mc, compiled, make_inputs) -> tuple[list, list]:
 
 
 def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0,
-              sampler: ClockSampler | None = None) -> dict:
+              sampler: ClockSampler | None = None, launches_first: bool = False) -> dict:
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
     # Graph replay captures once per binding: no rotation for it.
     rot, bufs = (None, None) if options and options.get("graph") else graph_rotation(mc, c, lambda: [x])
-    t = time_graph(mc, c, steps, warmup, rot, warm_seconds=warm_seconds, sampler=sampler)
+    t = time_graph(mc, c, steps, warmup, rot, warm_seconds=warm_seconds, sampler=sampler,
+                   launches_first=launches_first)
     work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
@@ -667,14 +688,15 @@ def main() -> int:
     sampler = ClockSampler(mc)
 
     if args.workload == "mlp":
-        r = bench_mlp(mc, args.batch, args.steps, args.warmup, sampler=sampler)
+        r = bench_mlp(mc, args.batch, args.steps, args.warmup, sampler=sampler, warm_seconds=WARM_SECONDS,
+                      launches_first=True)
         ks = r["kernels"]
         dom = max(ks, key=lambda e: e["ms"])
         line.update({"value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["timing"]["ms_per_step"],
                      "dtype": "f32",
                      "config": {"workload": f"mlp_gelu B={args.batch} D=512 H=2048 fp32 (BASELINE config 2)",
                                 "global_batch": args.batch, "matmul": ",".join(r["compiled"].matmul_kernels),
-                                "buffer_sets": r["buffer_sets"]},
+                                "buffer_sets": r["buffer_sets"], "order": r["timing"]["order"]},
                      "host_us_per_step": r["timing"]["host_us_per_step"]})
         unit = "TFLOP/s" if dom["bound"] == "mfma" else "GB/s"
         achieved = dom["tflops"] if dom["bound"] == "mfma" else dom["gbs"]

@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstring>
 #include <sstream>
+#include <utility>
 
 namespace minicompiler::hip {
 
@@ -56,13 +57,6 @@ std::string op_text(OpKind op, const std::string& a, const std::string& b) {
 
 std::string u32(std::size_t v) { return std::to_string(v) + "u"; }
 
-bool uses_op(const FusedProgram& program, OpKind op) {
-    for (const FusedInstr& ins : program.instrs) {
-        if ((ins.kind == FusedInstr::Kind::Unary || ins.kind == FusedInstr::Kind::Binary) && ins.op == op) return true;
-    }
-    return false;
-}
-
 // tanh in about 15 VALU instructions instead of the library's ~25, which
 // matters for GELU-shaped groups at HBM speed. For |x| < 0.625 an odd
 // polynomial x + x^3 P(x^2), P of degree 4 fitted here for relative error on
@@ -90,27 +84,123 @@ const char* const kTanhSource = R"(__device__ __forceinline__ float mc_tanh(floa
 
 )";
 
-// The program as a device function of its inputs' floats: one `const
-// float` per instruction, so with -ffp-contract=off every op rounds to float.
+// 1 + tanh(x) = 2 / (1 + e^{-2x}): one exp2 and one reciprocal, and no
+// cancellation as tanh(x) -> -1 (1 + tanh(x) computed in float loses every
+// significant bit there). About 3 ulp from the exact value.
+const char* const kOnePlusTanhSource = R"(__device__ __forceinline__ float mc_one_plus_tanh(float x)
+{
+	const float e = __builtin_amdgcn_exp2f(x * __uint_as_float(0xc038aa3bu) /* -2 log2(e) */);
+	return 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+)";
+
+// How each instruction of a program is emitted.
+struct Form {
+    enum class Kind : std::uint8_t { Plain, Absorbed, OnePlusTanh, Fma } kind = Kind::Plain;
+    // OnePlusTanh: x = tanh's operand. Fma: x * y + z (with `neg_x`: -x * y + z, `neg_z`: x * y - z).
+    std::int32_t x = -1, y = -1, z = -1;
+    bool neg_x = false, neg_z = false;
+};
+
+// Forms of the instructions of a multi-op program (a single op is emitted
+// as it is, so it rounds exactly as the reference's op does):
+// - an add of the immediate 1.0 and a tanh used only there becomes
+//   mc_one_plus_tanh of the tanh's operand;
+// - a mul used only by one add or sub becomes an fmaf there (one rounding
+//   instead of two), as NVRTC contracts a*b+c by default: the reference's
+//   run-time compile passes no option against it (src/cuda/kernel_compiler.cpp:35-37).
+std::vector<Form> program_forms(const FusedProgram& program) {
+    const std::size_t n = program.instrs.size();
+    std::vector<Form> forms(n);
+    if (program.num_ops() < 2) return forms;
+    std::vector<int> uses(n, 0);
+    for (const FusedInstr& ins : program.instrs) {
+        if (ins.kind == FusedInstr::Kind::Unary || ins.kind == FusedInstr::Kind::Binary) ++uses[ins.a];
+        if (ins.kind == FusedInstr::Kind::Binary) ++uses[ins.b];
+    }
+    ++uses[n - 1];
+    auto is = [&](std::int32_t r, OpKind op, FusedInstr::Kind kind) {
+        const FusedInstr& i = program.instrs[r];
+        return i.kind == kind && i.op == op && uses[r] == 1 && forms[r].kind == Form::Kind::Plain;
+    };
+    auto is_one = [&](std::int32_t r) {
+        const FusedInstr& i = program.instrs[r];
+        return i.kind == FusedInstr::Kind::Immediate && i.immediate == 1.0f;
+    };
+    for (std::size_t r = 0; r < n; ++r) {
+        const FusedInstr& ins = program.instrs[r];
+        if (ins.kind != FusedInstr::Kind::Binary) continue;
+        Form& f = forms[r];
+        if (ins.op == OpKind::Add) {
+            for (const auto& [t, k] : {std::pair{ins.a, ins.b}, std::pair{ins.b, ins.a}}) {
+                if (is(t, OpKind::Tanh, FusedInstr::Kind::Unary) && is_one(k)) {
+                    f = {Form::Kind::OnePlusTanh, program.instrs[t].a};
+                    forms[t].kind = Form::Kind::Absorbed;
+                    break;
+                }
+            }
+            if (f.kind != Form::Kind::Plain) continue;
+            for (const auto& [m, z] : {std::pair{ins.a, ins.b}, std::pair{ins.b, ins.a}}) {
+                if (is(m, OpKind::Mul, FusedInstr::Kind::Binary)) {
+                    f = {Form::Kind::Fma, program.instrs[m].a, program.instrs[m].b, z};
+                    forms[m].kind = Form::Kind::Absorbed;
+                    break;
+                }
+            }
+        } else if (ins.op == OpKind::Sub) {
+            if (is(ins.a, OpKind::Mul, FusedInstr::Kind::Binary)) {  // x y - z
+                f = {Form::Kind::Fma, program.instrs[ins.a].a, program.instrs[ins.a].b, ins.b, false, true};
+                forms[ins.a].kind = Form::Kind::Absorbed;
+            } else if (is(ins.b, OpKind::Mul, FusedInstr::Kind::Binary)) {  // z - x y
+                f = {Form::Kind::Fma, program.instrs[ins.b].a, program.instrs[ins.b].b, ins.a, true, false};
+                forms[ins.b].kind = Form::Kind::Absorbed;
+            }
+        }
+    }
+    return forms;
+}
+
+// The program as a device function of its inputs' floats, preceded by the
+// helper functions it calls: one `const float` per instruction, so with
+// -ffp-contract=off every op rounds to float, except where program_forms
+// fuses two instructions into one.
 std::string program_function(const FusedProgram& program, std::size_t num_inputs) {
+    const std::vector<Form> forms = program_forms(program);
+    bool tanh = false, one_plus_tanh = false;
+    std::ostringstream body;
+    auto reg = [](std::int32_t r) { return "r" + std::to_string(r); };
+    for (std::size_t r = 0; r < program.instrs.size(); ++r) {
+        const FusedInstr& ins = program.instrs[r];
+        const Form& f = forms[r];
+        if (f.kind == Form::Kind::Absorbed) continue;
+        body << "\tconst float r" << r << " = ";
+        if (f.kind == Form::Kind::OnePlusTanh) {
+            one_plus_tanh = true;
+            body << "mc_one_plus_tanh(" << reg(f.x) << ")";
+        } else if (f.kind == Form::Kind::Fma) {
+            body << "fmaf(" << (f.neg_x ? "-" : "") << reg(f.x) << ", " << reg(f.y) << ", " << (f.neg_z ? "-" : "")
+                 << reg(f.z) << ")";
+        } else {
+            switch (ins.kind) {
+                case FusedInstr::Kind::Load: body << "x" << ins.a; break;
+                case FusedInstr::Kind::Immediate: body << exact_float(ins.immediate); break;
+                case FusedInstr::Kind::Unary:
+                    tanh = tanh || ins.op == OpKind::Tanh;
+                    body << op_text(ins.op, reg(ins.a), "");
+                    break;
+                case FusedInstr::Kind::Binary: body << op_text(ins.op, reg(ins.a), reg(ins.b)); break;
+            }
+        }
+        body << ";\n";
+    }
     std::ostringstream os;
+    if (tanh) os << kTanhSource;
+    if (one_plus_tanh) os << kOnePlusTanhSource;
     os << "__device__ __forceinline__ float mc_program(";
     for (std::size_t k = 0; k < num_inputs; ++k) os << (k ? ", " : "") << "float x" << k;
     if (num_inputs == 0) os << "void";
-    os << ")\n{\n";
-    for (std::size_t r = 0; r < program.instrs.size(); ++r) {
-        const FusedInstr& ins = program.instrs[r];
-        os << "\tconst float r" << r << " = ";
-        switch (ins.kind) {
-            case FusedInstr::Kind::Load: os << "x" << ins.a; break;
-            case FusedInstr::Kind::Immediate: os << exact_float(ins.immediate); break;
-            case FusedInstr::Kind::Unary: os << op_text(ins.op, "r" + std::to_string(ins.a), ""); break;
-            case FusedInstr::Kind::Binary:
-                os << op_text(ins.op, "r" + std::to_string(ins.a), "r" + std::to_string(ins.b));
-                break;
-        }
-        os << ";\n";
-    }
+    os << ")\n{\n" << body.str();
     os << "\treturn r" << program.instrs.size() - 1 << ";\n}\n\n";
     return os.str();
 }
@@ -160,7 +250,6 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
        << " GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
        << to_string(out_shape) << ".\n";
     os << gemm_body_source << "\n";
-    if (uses_op(program, OpKind::Tanh)) os << kTanhSource;
     os << program_function(program, num_inputs);
     // Index helpers of General inputs, in terms of the flat output index i.
     for (std::size_t k = 0; k < num_inputs; ++k) {
@@ -298,7 +387,6 @@ ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const
        << to_string(out_shape) << ", " << (vec ? "16-byte vector accesses" : "scalar accesses") << ", " << per_lane
        << " item(s) per lane per step.\n";
     os << "typedef float mc_f32x4 __attribute__((ext_vector_type(4)));\n\n";
-    if (uses_op(program, OpKind::Tanh)) os << kTanhSource;
 
     os << program_function(program, num_inputs);
 

@@ -37,9 +37,36 @@ def test_fused_gelu_is_one_vectorised_kernel(mc):
     # Exact bit patterns, once, in the program (before the kernel's loop).
     assert src.count("__uint_as_float(0x3f000000u)") == 1
     assert src.index("0x3f000000u") < kernel_loop(src)
-    assert src.count("mc_tanh(r") == 1            # once in the program ...
-    assert src.count("float mc_tanh(float x)") == 1  # (the generator's own tanh, defined once)
+    # 1 + tanh(u) is one mc_one_plus_tanh, x + x^3 coef one fmaf, in the program ...
+    assert src.count("mc_one_plus_tanh(r") == 1 and "mc_tanh" not in src
+    assert src.count("float mc_one_plus_tanh(float x)") == 1  # (defined once)
+    assert src.count("fmaf(") == 1
     assert src.count("mc_program(a0[u].") == 8     # ... applied to 4 lanes, full and ragged steps
+
+
+def program_of(src):
+    return src[src.index("float mc_program("):src.index("extern")]
+
+
+def test_multi_op_programs_contract_a_mul_used_once_into_its_add_or_sub(mc):
+    shapes = [(64,), (64,), (64,)]
+    # x y + z, z - x y, x y - z: one fmaf each, the mul not emitted alone.
+    for text, call in (("r3 = mul r0, r1\nr4 = add r3, r2\n", "fmaf(r0, r1, r2)"),
+                       ("r3 = mul r0, r1\nr4 = sub r2, r3\n", "fmaf(-r0, r1, r2)"),
+                       ("r3 = mul r0, r1\nr4 = sub r3, r2\n", "fmaf(r0, r1, -r2)")):
+        src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = load in1\nr2 = load in2\n" + text, shapes, (64,))
+        body = program_of(src)
+        assert f"const float r4 = {call};" in body and "const float r3" not in body, body
+    # A mul with a second use stays a mul (and its add an add); a single op is never rewritten.
+    src, _ = mc.generate_elementwise_kernel(
+        "r0 = load in0\nr1 = load in1\nr2 = load in2\nr3 = mul r0, r1\nr4 = add r3, r2\nr5 = mul r4, r3\n", shapes, (64,))
+    assert "fmaf" not in program_of(src)
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = load in1\nr2 = mul r0, r1\n", shapes[:2], (64,))
+    assert "fmaf" not in program_of(src) and "const float r2 = r0 * r1;" in src
+    # tanh plus an immediate other than 1, or a tanh used twice: the plain tanh.
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = imm 2.0\nr2 = tanh r0\nr3 = add r2, r1\n",
+                                            shapes[:1], (64,))
+    assert "mc_one_plus_tanh" not in src and "mc_tanh(r0)" in src
 
 
 def test_reads_a_bias_row_periodically(mc):

@@ -66,8 +66,8 @@ struct HipOptions {
     bool vectorize = true;
     // Elementwise kernel shape: vectors (or floats) each lane has in flight
     // per loop step, non-temporal hints on the streaming loads and stores,
-    // and resident blocks per CU the grid is sized for (0: the occupancy
-    // the runtime reports).
+    // and the grid's blocks per CU (more than fit at once run in turn;
+    // 0: 64, so in practice one loop step per block), capped by the work.
     unsigned elementwise_items = 4;
     bool nontemporal_loads = true;
     bool nontemporal_stores = true;

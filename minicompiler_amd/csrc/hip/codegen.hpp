@@ -25,6 +25,8 @@ namespace minicompiler::hip {
 inline constexpr const char* kElementwiseKernelName = "mc_elementwise";
 // Lanes per block: four 64-wide waves. The generated kernel assumes it.
 inline constexpr unsigned kElementwiseBlock = 256;
+// Default cap of the elementwise grid, in blocks per CU.
+inline constexpr int kElementwiseBlocksPerCu = 64;
 
 struct CodegenOptions {
     // 16-byte accesses when every input allows them.

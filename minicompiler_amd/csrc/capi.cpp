@@ -748,6 +748,8 @@ MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, 
         {"ring_thin", hip::GemmBody::F32RingThin, &hip::kGemmF32RingSource},
         {"narrow16", hip::GemmBody::F32Narrow16, &hip::kGemmF32NarrowSource},
         {"narrow32", hip::GemmBody::F32Narrow32, &hip::kGemmF32NarrowSource},
+        {"narrow16x64", hip::GemmBody::F32Narrow16x64, &hip::kGemmF32NarrowSource},
+        {"narrow16x32", hip::GemmBody::F32Narrow16x32, &hip::kGemmF32NarrowSource},
         {"bf16", hip::GemmBody::Bf16Fast, &hip::kGemm16FastSource},
         {"f16", hip::GemmBody::F16Fast, &hip::kGemm16FastSource},
     };

@@ -307,7 +307,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         os << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false") << ">(a, b, c, " << mnk
            << ", " << (constant ? std::to_string(fixed.k_split) : std::string("k_split")) << ", partial, epi);\n}\n\n";
     } else if (is_narrow_body(body)) {
-        os << "\tmc_gemm_f32_narrow<" << (body == GemmBody::F32Narrow16 ? "McNarrow16" : "McNarrow32") << ">(a, b, c, "
+        os << "\tmc_gemm_f32_narrow<" << narrow_config(body) << ">(a, b, c, "
            << mnk << ", " << split << ", partial, epi);\n}\n\n";
     } else {
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"

@@ -30,7 +30,7 @@
 // (summed afterwards in range order, the epilogue applied there).
 //
 // Requirements (checked by the host): k and k_split multiples of 16, n a
-// multiple of kVec, A and B 16-byte aligned (C and the partials may be at
+// multiple of kVec (the host asks for 4), A and B 16-byte aligned (C and the partials may be at
 // any float address). Rows past m read
 // row m - 1 and columns past n the last column chunk (every load in
 // bounds); what they produce is not stored.
@@ -68,10 +68,16 @@ struct McNarrowCfg {
     static constexpr int kRows = 16 * kRG, kCols = 16 * kVec, kThreads = 64 * kW;
 };
 
-// The configurations the library runs: 16x64 tiles for M <= 16 and 32x64
-// tiles, 4 waves each.
+// The configurations the library runs, 4 waves each: 16x64 tiles for
+// M <= 16 (B streamed), 32x64 tiles, and for short-K products that these
+// would leave with half the CUs idle, 16x64 and 16x32 tiles (the latter
+// with batches of 2 groups). At one K range every configuration adds the
+// same products in the same order (per element: the 4 waves' pieces of K in
+// wave order, each a chain of 16x16x4 MFMAs), so they give the same bits.
 using McNarrow16 = McNarrowCfg<1, 4, 4, 4, true>;
 using McNarrow32 = McNarrowCfg<2, 4, 4, 4, false>;
+using McNarrow16x64 = McNarrowCfg<1, 4, 4, 4, false>;
+using McNarrow16x32 = McNarrowCfg<1, 2, 4, 2, false>;
 
 // One batch of a wave's operands: kU groups of 16 k.
 template <class Cfg>

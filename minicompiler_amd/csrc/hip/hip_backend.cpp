@@ -528,12 +528,17 @@ private:
         if (l.lowp) return l.dtype == MCHIP_DTYPE_BF16 ? GemmBody::Bf16Fast : GemmBody::F16Fast;
         if (l.matmul == MatmulKernel::SplitK &&
             (l.ring_cfg == MCHIP_RING_NONE || l.ring_cfg == MCHIP_RING_NARROW)) {
-            int rows = 0, splits = 0, k_split = 0;
+            int shape = 0, splits = 0, k_split = 0;
             if (mchip_f32_narrow_plan(l.m, l.n, l.k, std::max(l.splits, 1), device_.cu_count,
-                                      l.ring_cfg == MCHIP_RING_NARROW, &rows, &splits, &k_split)) {
+                                      l.ring_cfg == MCHIP_RING_NARROW, &shape, &splits, &k_split)) {
                 l.k_split = k_split;
                 l.depth = splits;
-                return rows == 16 ? GemmBody::F32Narrow16 : GemmBody::F32Narrow32;
+                switch (shape) {
+                    case MCHIP_NARROW_16X64_STREAM: return GemmBody::F32Narrow16;
+                    case MCHIP_NARROW_16X64: return GemmBody::F32Narrow16x64;
+                    case MCHIP_NARROW_16X32: return GemmBody::F32Narrow16x32;
+                    default: return GemmBody::F32Narrow32;
+                }
             }
         }
         split_layout(l.k, l.splits, &l.k_split, &l.depth);
@@ -684,8 +689,8 @@ private:
                     l.block = 256;
                 } else if (is_narrow_body(l.body)) {
                     // One-dimensional: the body maps blocks to tiles XCD by XCD.
-                    const int rows = l.body == GemmBody::F32Narrow16 ? 16 : 32;
-                    l.grid_x = static_cast<unsigned>(((l.n + 63) / 64) * l.depth * ((l.m + rows - 1) / rows));
+                    const int rows = narrow_rows(l.body), cols = narrow_cols(l.body);
+                    l.grid_x = static_cast<unsigned>(((l.n + cols - 1) / cols) * l.depth * ((l.m + rows - 1) / rows));
                     l.grid_y = l.grid_z = 1;
                     l.block = 256;
                 } else {

@@ -69,16 +69,28 @@ enum {
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);
 
-/* The narrow-tile body (gemm_f32_narrow.h), which the split_k rung runs for
- * products whose 32x64 tiles (16x64 for m <= 16) number at most one per CU:
- * K is cut into *splits ranges of *k_split (a multiple of 16), at most
+/* The narrow-tile body (gemm_f32_narrow.h) in its tile shapes. */
+enum {
+    MCHIP_NARROW_32X64 = 0,         /* 32x64 tiles */
+    MCHIP_NARROW_16X64_STREAM = 1,  /* 16x64 tiles, B streamed: m <= 16 */
+    MCHIP_NARROW_16X64 = 2,         /* 16x64 tiles */
+    MCHIP_NARROW_16X32 = 3,         /* 16x32 tiles */
+};
+int mchip_narrow_rows(int shape);
+int mchip_narrow_cols(int shape);
+
+/* The narrow-tile body, which the split_k rung runs for products whose
+ * tiles number at most one per CU. With K <= 2048, a tile shape that gives
+ * more than half the CUs a tile runs unsplit (the first of 32x64, 16x64,
+ * 16x32 that does); otherwise 32x64 tiles (16x64, B streamed, for m <= 16)
+ * with K cut into *splits ranges of *k_split (a multiple of 16), at most
  * max_splits of them, so that tiles x ranges stays within the CUs. Its
  * accumulation order is its own (16x16x4 MFMAs, K pieces per wave added
  * in wave order, then the ranges in range order), not the ring body's.
- * Returns 1 and fills *rows (16 or 32), *splits and *k_split when the plan
- * runs the product on it (force: whenever the shape fits: k a multiple of
- * 16, n of 4), else 0. */
-int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* rows, int* splits,
+ * Returns 1 and fills *shape (MCHIP_NARROW_*), *splits and *k_split when
+ * the plan runs the product on it (force: whenever the shape fits: k a
+ * multiple of 16, n of 4), else 0. */
+int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* shape, int* splits,
                           int* k_split);
 
 /* The narrow-tile body directly: `rows` 16 (m <= 16) or 32, K in `splits`

@@ -236,21 +236,28 @@ int device_cu_count() {
     return cus;
 }
 
-// The narrow-tile body on `depth` K ranges of k_split, the partials summed
-// in range order when there are several.
-int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int rows,
+template <class Cfg>
+void narrow_kernel(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int k_split,
+                   int depth, float* part) {
+    const dim3 grid(((n + Cfg::kCols - 1) / Cfg::kCols) * depth * ((m + Cfg::kRows - 1) / Cfg::kRows));
+    hipLaunchKernelGGL((matmul_narrow_f32<Cfg>), grid, dim3(Cfg::kThreads), 0, s, a, b, c, m, n, k, k_split, depth,
+                       part);
+}
+
+// The narrow-tile body in tile shape `shape` on `depth` K ranges of
+// k_split, the partials summed in range order when there are several.
+int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int shape,
                   int k_split, int depth, float* workspace) {
     float* dst = depth > 1 ? workspace : c;
     if (!aligned16(a) || !aligned16(b) || dst == nullptr) return hipErrorInvalidValue;
+    if (shape == MCHIP_NARROW_16X64_STREAM && m > 16) return hipErrorInvalidValue;
     float* part = depth > 1 ? workspace : nullptr;
-    if (rows == 16) {
-        const dim3 grid(((n + McNarrow16::kCols - 1) / McNarrow16::kCols) * depth * ((m + 15) / 16));
-        hipLaunchKernelGGL((matmul_narrow_f32<McNarrow16>), grid, dim3(McNarrow16::kThreads), 0, s, a, b, c, m, n, k,
-                           k_split, depth, part);
-    } else {
-        const dim3 grid(((n + McNarrow32::kCols - 1) / McNarrow32::kCols) * depth * ((m + 31) / 32));
-        hipLaunchKernelGGL((matmul_narrow_f32<McNarrow32>), grid, dim3(McNarrow32::kThreads), 0, s, a, b, c, m, n, k,
-                           k_split, depth, part);
+    switch (shape) {
+        case MCHIP_NARROW_32X64: narrow_kernel<McNarrow32>(a, b, c, m, n, k, s, k_split, depth, part); break;
+        case MCHIP_NARROW_16X64_STREAM: narrow_kernel<McNarrow16>(a, b, c, m, n, k, s, k_split, depth, part); break;
+        case MCHIP_NARROW_16X64: narrow_kernel<McNarrow16x64>(a, b, c, m, n, k, s, k_split, depth, part); break;
+        case MCHIP_NARROW_16X32: narrow_kernel<McNarrow16x32>(a, b, c, m, n, k, s, k_split, depth, part); break;
+        default: return hipErrorInvalidValue;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || depth == 1) return e;
@@ -262,11 +269,11 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     // split_k on the narrow-tile body when the plan (or the caller) takes it,
     // with at most the caller's split count (its workspace's size).
     if (split_k && (ring_cfg == MCHIP_RING_NONE || ring_cfg == MCHIP_RING_NARROW) && aligned16(a) && aligned16(b)) {
-        int rows = 0, ns = 0, nk = 0;
+        int shape = 0, ns = 0, nk = 0;
         if (mchip_f32_narrow_plan(m, n, k, std::max(splits, 1), device_cu_count(), ring_cfg == MCHIP_RING_NARROW,
-                                  &rows, &ns, &nk)) {
+                                  &shape, &ns, &nk)) {
             if (ns > 1 && workspace == nullptr) return hipErrorInvalidValue;  // as the ring would
-            return launch_narrow(a, b, c, m, n, k, stream, rows, nk, ns, workspace);
+            return launch_narrow(a, b, c, m, n, k, stream, shape, nk, ns, workspace);
         }
     }
     if (ring_cfg == MCHIP_RING_NARROW) return hipErrorInvalidValue;
@@ -372,12 +379,43 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     return mchip_f32_ring_plan_cfg(m, n, k, depth, cu_count, MCHIP_RING_NONE, grid, block);
 }
 
-extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* rows,
+extern "C" int mchip_narrow_rows(int shape) {
+    return shape == MCHIP_NARROW_32X64 ? 32 : 16;
+}
+
+extern "C" int mchip_narrow_cols(int shape) {
+    return shape == MCHIP_NARROW_16X32 ? 32 : 64;
+}
+
+extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu_count, int force, int* shape,
                                      int* splits, int* k_split) {
-    *rows = *splits = *k_split = 0;
+    *shape = *splits = *k_split = 0;
     if (m < 1 || n < 4 || n % 4 != 0 || k < 16 || k % 16 != 0 || max_splits < 1 || cu_count < 1) return 0;
-    const int r = m <= 16 ? 16 : 32;
-    const long long tiles = static_cast<long long>((m + r - 1) / r) * ((n + 63) / 64);
+    auto tiles_of = [&](int sh) {
+        return static_cast<long long>((m + mchip_narrow_rows(sh) - 1) / mchip_narrow_rows(sh)) *
+               ((n + mchip_narrow_cols(sh) - 1) / mchip_narrow_cols(sh));
+    };
+    // Short K: the first tile shape that gives more than half the CUs a
+    // tile runs unsplit, one block per CU with no partials and no sum
+    // launch. Measured on an MI355X (launch plus sum, one operand set):
+    // 256x512x2048 on 16x32 tiles 9.6 us against 11.2 on 32x64 tiles in 4
+    // ranges; 512^3 on 16x64 tiles 5.4 against 8.3 on 32x64 unsplit. With
+    // longer K the smaller tiles' extra operand traffic costs more than a
+    // sum launch (256x256x16384: 32.6 us on 16x32 tiles in 2 ranges against
+    // 24.8 on 32x64 in 8).
+    if (m > 16 && k <= 2048) {
+        for (int sh : {MCHIP_NARROW_32X64, MCHIP_NARROW_16X64, MCHIP_NARROW_16X32}) {
+            const long long t = tiles_of(sh);
+            if (2 * t > cu_count && t <= cu_count) {
+                *shape = sh;
+                *k_split = k;
+                *splits = 1;
+                return 1;
+            }
+        }
+    }
+    const int sh = m <= 16 ? MCHIP_NARROW_16X64_STREAM : MCHIP_NARROW_32X64;
+    const long long tiles = tiles_of(sh);
     // Measured on an MI355X (one-matmul launches, operands past the MALL):
     // against the ring body, the narrow body wins while its tiles fit one
     // per CU (256x2048x512: 9.4 against 16.2 us; 256x512x2048 in 4 ranges
@@ -391,7 +429,7 @@ extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu
     int s = 1;
     while (s * 2 <= max_splits && tiles * s * 2 <= cu_count && k / (s * 2) >= 64) s *= 2;
     const int ks = ((k + s - 1) / s + 15) / 16 * 16;
-    *rows = r;
+    *shape = sh;
     *k_split = ks;
     *splits = (k + ks - 1) / ks;
     return 1;
@@ -402,8 +440,9 @@ extern "C" int mchip_launch_narrow(const float* a, const float* b, float* c, int
     if (m < 1 || n < 4 || n % 4 != 0 || k < 16 || k % 16 != 0 || splits < 1) return hipErrorInvalidValue;
     if ((rows != 16 && rows != 32) || (rows == 16 && m > 16)) return hipErrorInvalidValue;
     const int k_split = ((k + splits - 1) / splits + 15) / 16 * 16;
-    return launch_narrow(a, b, c, m, n, k, static_cast<hipStream_t>(stream), rows, k_split, (k + k_split - 1) / k_split,
-                         workspace);
+    return launch_narrow(a, b, c, m, n, k, static_cast<hipStream_t>(stream),
+                         rows == 16 ? MCHIP_NARROW_16X64_STREAM : MCHIP_NARROW_32X64, k_split,
+                         (k + k_split - 1) / k_split, workspace);
 }
 
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {

@@ -157,6 +157,8 @@ def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, ou
                                        ("ring_mid", "mc_gemm_f32_ring<McRingMid>"),
                                        ("narrow16", "mc_gemm_f32_narrow<McNarrow16>"),
                                        ("narrow32", "mc_gemm_f32_narrow<McNarrow32>"),
+                                       ("narrow16x64", "mc_gemm_f32_narrow<McNarrow16x64>"),
+                                       ("narrow16x32", "mc_gemm_f32_narrow<McNarrow16x32>"),
                                        ("bf16", "mc_gemm16_fast<true>"), ("f16", "mc_gemm16_fast<false>")])
 def test_every_gemm_body_with_an_epilogue_compiles_for_gfx950(mc, body, call):
     # bias + tanh on the product, as a fused group reads it: each GEMM body the

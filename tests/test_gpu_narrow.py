@@ -20,8 +20,11 @@ GUARD = 4096
 # (m, k, n, splits): one row, M < 16, exactly 16, ragged M past a 32-row
 # tile, N not a multiple of 64 (and not of 8), K not a multiple of the
 # split, a split count above what the plan would take, the bench shapes.
+# The short-K tile shapes too: 256x2048x512 and 300x96x260 on 16x32 tiles,
+# 512^3 and 200x512x640 (ragged M) on 16x64 tiles, unsplit.
 SHAPES = [(1, 16, 4, 1), (5, 96, 260, 3), (16, 4096, 4096, 8), (33, 1040, 1000, 4), (300, 96, 260, 2),
-          (256, 512, 2048, 8), (256, 2048, 512, 32), (512, 512, 512, 8), (16, 64, 68, 64), (256, 16384, 256, 64)]
+          (256, 512, 2048, 8), (256, 2048, 512, 32), (512, 512, 512, 8), (16, 64, 68, 64), (256, 16384, 256, 64),
+          (200, 512, 640, 4)]
 
 
 def run(mc, ring, a, b, m, k, n, splits):
@@ -80,7 +83,7 @@ def test_a_forced_narrow_launch_the_product_cannot_take_is_an_error(device, mc):
 
 
 GRAPHS = [("mlp_gelu", {"B": 256}), ("mlp_gelu", {"B": 16}), ("matmul_bias_relu", {"M": 16, "K": 1024, "N": 1000}),
-          ("matmul_bias_relu", {"M": 96, "K": 512, "N": 512})]
+          ("matmul_bias_relu", {"M": 96, "K": 512, "N": 512}), ("matmul_bias_relu", {"M": 512, "K": 512, "N": 512})]
 
 
 @pytest.mark.parametrize("name,dims", GRAPHS)
@@ -101,3 +104,16 @@ def test_graphs_on_narrow_tiles_fuse_their_groups_bit_for_bit_and_match_the_orac
     cpu = oracle.evaluate_compiled(fused, inputs)
     for p, c in zip(x, cpu):
         assert_close(p, c, 1e-4, 1e-4 * max(1.0, max_abs(c)), f"{name} {dims}")
+
+
+def test_short_k_products_run_on_the_tile_shape_that_gives_most_cus_a_tile(device, mc):
+    # On 256 CUs: the MLP at B=256 runs GEMM1 (256x2048x512) on 32x64 tiles
+    # and GEMM2 (256x512x2048) on 16x32 tiles, 512^3 on 16x64 tiles.
+    if int(device["cu_count"]) != 256:
+        pytest.skip("tile counts are for 256 CUs")
+    opts = {"matmul": "split_k"}
+    mlp = "\n".join(mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": 256}, options=opts).kernel_sources)
+    assert "mc_gemm_f32_narrow<McNarrow32>" in mlp and "mc_gemm_f32_narrow<McNarrow16x32>" in mlp
+    sq = "\n".join(mc.Compiled(path=mc.graph_path("matmul_bias_relu"), dims={"M": 512, "K": 512, "N": 512},
+                               options=opts).kernel_sources)
+    assert "mc_gemm_f32_narrow<McNarrow16x64>" in sq

@@ -469,6 +469,21 @@ def sample_rows(full: int, first: int, per_call, target_s: float = 0.25) -> int:
     return int(max(1, min(full, round(first * target_s / el))))
 
 
+def host_cpu() -> dict:
+    """The host's CPU model and logical core count, recorded with every CPU
+    baseline (bench/harness.hpp:194-205, 246)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "hardware_concurrency": os.cpu_count()}
+
+
 def cpu_entry(per_row_work: float, unit: str, rows: int, full_rows: int, cap_rows: int, call_of, what: str,
               seconds: float) -> dict:
     """One-thread timing of call_of(rows)() and, on this GPU's host share,
@@ -491,7 +506,8 @@ def cpu_entry(per_row_work: float, unit: str, rows: int, full_rows: int, cap_row
                       f"oracle/cpu_oracle.cpp + cpu_gemm.cpp (Eigen semantics, own GEMM; Eigen is not on the box), "
                       f"1 thread, {os.cpu_count()} host cores",
             "all_cores": {"value": va, "threads": threads,
-                          "sample": f"rows 0..{ra - 1}, {repsa} calls, median {pera * 1e3:.2f} ms/call"}}
+                          "sample": f"rows 0..{ra - 1}, {repsa} calls, median {pera * 1e3:.2f} ms/call"},
+            "host": host_cpu()}
 
 
 def cpu_baseline_graph(mc, name: str, dims_of, full_rows: int, row_elems: int, make_input, per_row_work: float,

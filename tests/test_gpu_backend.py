@@ -85,6 +85,29 @@ def test_tanh_over_a_dense_range_and_its_special_values(device, mc, oracle):
     assert np.all(np.isnan(c4.run([np.full(4, np.nan, np.float32)])[0]))
 
 
+def test_one_plus_tanh_in_a_fused_group_over_a_dense_range(device, mc):
+    # A group's 1 + tanh(x) is emitted as 2 / (1 + 2^(-2 x log2 e)) (one
+    # exp2, one reciprocal): against float64, within 4 ulp plus the exp2
+    # argument's rounding (of the constant 2 log2(e) and of its product with
+    # x: 2 |x| 2 log2(e) 2^-24, times ln 2, relative), with no cancellation
+    # as tanh(x) -> -1; +-inf and NaN as 1 + tanh gives them.
+    xs = np.concatenate([np.linspace(-60, 60, 96001, dtype=np.float32),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 1e30, -1e30, np.inf, -np.inf], np.float32)])
+    c = mc.Compiled(f"input x : f32[{xs.size}]\nconst one : f32[] = 1.0\nt = tanh x\ny = add t, one\noutput y\n")
+    (src,) = c.kernel_sources
+    assert "mc_one_plus_tanh(r" in src and "mc_tanh(" not in src
+    gpu = c.run([xs])[0].astype(np.float64)
+    x64 = xs.astype(np.float64)
+    with np.errstate(over="ignore"):
+        ref = 2.0 / (1.0 + np.exp(-2.0 * x64))  # = 1 + tanh(x), without float64's own cancellation
+    fin = np.isfinite(x64)
+    bound = (4 * 2.0**-24 + 2 * np.abs(np.where(fin, x64, 0.0)) * 2.0 * np.log2(np.e) * 2.0**-24 * np.log(2)) * ref + 1e-37
+    bad = np.where(fin, np.abs(gpu - ref) > bound, gpu != ref)  # 1 + tanh(+-inf) = 2, 0 exactly
+    assert not np.any(bad), (xs[bad][:5], gpu[bad][:5], ref[bad][:5])
+    nan = mc.Compiled("input x : f32[4]\nconst one : f32[] = 1.0\nt = tanh x\ny = add t, one\noutput y\n")
+    assert np.all(np.isnan(nan.run([np.full(4, np.nan, np.float32)])[0]))
+
+
 @pytest.mark.parametrize("sa,sb", PATTERNS)
 def test_binary_ops_match_bit_for_bit_for_every_broadcast_pattern(device, mc, oracle, sa, sb):
     for op in BINARY:

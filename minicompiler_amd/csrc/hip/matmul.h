@@ -69,6 +69,13 @@ enum {
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);
 
+/* 1 when a split_k product asked to split K (splits > 1) runs faster
+ * unsplit on the ring's 64x128 tiles (MCHIP_RING_MID): K <= 1024 and those
+ * tiles number more than half the CUs and at most all of them. The split_k
+ * rung then does so (when A, B and C are 16-byte aligned and the caller
+ * forces no configuration), in place of the split rule's count. */
+int mchip_f32_unsplit_ring(int m, int n, int k, int splits, int cu_count);
+
 /* The narrow-tile body (gemm_f32_narrow.h) in its tile shapes. */
 enum {
     MCHIP_NARROW_32X64 = 0,         /* 32x64 tiles */

@@ -277,6 +277,11 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
         }
     }
     if (ring_cfg == MCHIP_RING_NARROW) return hipErrorInvalidValue;
+    if (split_k && ring_cfg == MCHIP_RING_NONE && aligned16(a) && aligned16(b) && aligned16(c) &&
+        mchip_f32_unsplit_ring(m, n, k, splits, device_cu_count())) {
+        splits = 1;
+        ring_cfg = MCHIP_RING_MID;
+    }
     const int k_split = split_len(k, splits, kMBK);
     const int depth = std::max(1, (k + k_split - 1) / k_split);
     if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
@@ -377,6 +382,19 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
 
 extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block) {
     return mchip_f32_ring_plan_cfg(m, n, k, depth, cu_count, MCHIP_RING_NONE, grid, block);
+}
+
+extern "C" int mchip_f32_unsplit_ring(int m, int n, int k, int splits, int cu_count) {
+    // Measured on an MI355X (same process, operands past the MALL, graph-timed
+    // launch plus sum): 1024x2048x512 unsplit on 64x128 tiles 24.2 us against
+    // 28.7 us for the rule's 2 splits on 128x128 tiles; 2048x1024x512 24.2
+    // against 28.6; 768x2048x512 23.8 against 27.4; 1024x2048x1024 43.6
+    // against 44.7. Where 64x128 tiles leave half the CUs idle, or K is
+    // longer, the split wins (1024^3: 42.8 against 28.0; 1024x1024x4096:
+    // 160.3 against 75.9).
+    if (splits < 2 || cu_count < 1 || m < 1 || n % 4 != 0 || k % 32 != 0 || k > 1024) return 0;
+    const long long tiles = static_cast<long long>((m + 63) / 64) * ((n + 127) / 128);
+    return 2 * tiles > cu_count && tiles <= cu_count ? 1 : 0;
 }
 
 extern "C" int mchip_narrow_rows(int shape) {

@@ -116,6 +116,31 @@ def test_forced_ring_configurations_give_the_plans_bits(device, mc, oracle, m, k
     assert np.all(np.abs(planned.astype(np.float64) - exact) <= bound)
 
 
+def test_split_k_runs_unsplit_on_64x128_tiles_where_they_fill_the_cus(device, mc, oracle):
+    # 1024x512x2048 (m, k, n): the split rule asks for 2 splits on 256 CUs; 64x128
+    # tiles number 256, so the split_k rung runs it unsplit on the mid
+    # configuration: the bits of a forced mid launch with one split (not
+    # those of the rule's two), within the dot-product bound.
+    m, k, n = 1024, 512, 2048
+    if int(device["cu_count"]) != 256:
+        pytest.skip("tile counts are for 256 CUs")
+    splits = mc.matmul_splits("split_k", m, n, k, 256)
+    assert splits == 2
+    a = oracle.uniform(m * k, 23, -1.0, 1.0)
+    b = oracle.uniform(k * n, 24, -1.0, 1.0)
+    da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
+    ws = mc.DeviceBuffer(mc.matmul_workspace_bytes("split_k", m, n, splits))
+    planned = run_cfg(mc, "split_k", "auto", da, db, m, n, k, splits, ws)
+    unsplit = run_cfg(mc, "split_k", "mid", da, db, m, n, k, 1, None)
+    assert np.array_equal(planned.view(np.uint32), unsplit.view(np.uint32))
+    split = run_cfg(mc, "split_k", "wide", da, db, m, n, k, splits, ws)
+    assert not np.array_equal(planned.view(np.uint32), split.view(np.uint32))
+    rows = np.arange(0, m, 7)
+    exact, absdot = oracle.gemm_f64(a.reshape(m, k)[rows].ravel(), b, rows.size, k, n)
+    assert np.all(np.abs(planned.reshape(m, n)[rows].astype(np.float64).ravel() - exact) <=
+                  fp32_gemm_bound(exact, absdot, k))
+
+
 def test_a_forced_configuration_the_product_cannot_take_is_an_error(device, mc):
     # K not a multiple of 32: no ring configuration runs it.
     da, db, dc = mc.DeviceBuffer(4 * 64 * 40), mc.DeviceBuffer(4 * 40 * 64), mc.DeviceBuffer(4 * 64 * 64)

@@ -68,7 +68,7 @@ struct HipOptions {
     // per loop step, non-temporal hints on the streaming loads and stores,
     // and the grid's blocks per CU (more than fit at once run in turn;
     // 0: 64, so in practice one loop step per block), capped by the work.
-    unsigned elementwise_items = 4;
+    unsigned elementwise_items = 0;  // 0: by the program (8 for 8 or more ops, else 4)
     bool nontemporal_loads = true;
     bool nontemporal_stores = true;
     unsigned elementwise_blocks_per_cu = 0;

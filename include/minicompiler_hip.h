@@ -151,7 +151,9 @@ MC_API int mc_print_graph(const void* handle, char* out, int size);
 /* The kernel generator (codegen.hpp:34-40): `program` in the printed form,
  * one instruction per line ("r0 = load in0", "r1 = imm 0x3f000000" (bits) or
  * "r1 = imm 0.5", "r2 = mul r0, r1"); `input_shapes` as "[8,64];[64];[]";
- * `out_shape` as "[8,64]". *vectorized receives 1 for 16-byte accesses. */
+ * `out_shape` as "[8,64]"; items_per_lane <= 0: the generator's choice (8
+ * for programs of 8 or more ops, else 4). *vectorized receives 1 for
+ * 16-byte accesses. */
 MC_API int mc_generate_elementwise_kernel(const char* program, const char* input_shapes, const char* out_shape,
                                           int allow_vectorize, int items_per_lane, int* vectorized, char* out,
                                           int size);

@@ -115,7 +115,7 @@ Result<hip::HipOptions> parse_options(const char* spec) {
         } else if (key == "ew_items" || key == "ew_blocks_per_cu") {
             Result<long long> v = to_integer(value);
             if (!v.ok()) return v.error();
-            if (v.value() < 0 || v.value() > 64 || (key == "ew_items" && v.value() < 1)) {
+            if (v.value() < 0 || v.value() > 64) {
                 return Error{"option " + key + " out of range: " + value};
             }
             (key == "ew_items" ? o.elementwise_items : o.elementwise_blocks_per_cu) = static_cast<unsigned>(v.value());

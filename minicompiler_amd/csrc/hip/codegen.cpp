@@ -347,7 +347,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
 CodegenOptions codegen_options(const HipOptions& options) {
     CodegenOptions cg;
     cg.allow_vectorize = options.vectorize;
-    cg.items_per_lane = std::max(1u, options.elementwise_items);
+    cg.items_per_lane = options.elementwise_items;
     cg.nontemporal_loads = options.nontemporal_loads;
     cg.nontemporal_stores = options.nontemporal_stores;
     return cg;
@@ -379,7 +379,7 @@ ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const
         if (a.kind == Access::Kind::General) vec = false;
         if (a.kind == Access::Kind::Periodic && a.period % 4 != 0) vec = false;
     }
-    const unsigned per_lane = std::max(1u, options.items_per_lane);
+    const unsigned per_lane = options.items_per_lane > 0 ? options.items_per_lane : program.num_ops() >= 8 ? 8u : 4u;
     const std::string item = vec ? "mc_f32x4" : "float";
 
     std::ostringstream os;

@@ -32,8 +32,12 @@ struct CodegenOptions {
     // 16-byte accesses when every input allows them.
     bool allow_vectorize = true;
     // Vectors (or floats) each lane loads before it computes and stores: more
-    // bytes in flight per wave to cover HBM latency.
-    unsigned items_per_lane = 4;
+    // bytes in flight per wave to cover HBM latency. 0: by the program, 8
+    // for programs of 8 or more ops (their arithmetic holds back each wave's
+    // stores), else 4 (measured on an MI355X: GELU 4096^2 5.95 TB/s with 8
+    // against 5.88 with 4; BatchNorm 6.19 with 4 against 6.10 with 8; copy
+    // 6.28 with 4 against 6.08).
+    unsigned items_per_lane = 0;
     // Non-temporal hints on the streaming loads and stores.
     bool nontemporal_loads = true;
     bool nontemporal_stores = true;

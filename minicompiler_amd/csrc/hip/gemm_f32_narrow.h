@@ -1,5 +1,6 @@
-// FP32 GEMM body for narrow tiles: C tiles of 16 kRG rows x 64 columns on
-// v_mfma_f32_16x16x4f32, for products too small or too thin to fill the chip
+// FP32 GEMM body for narrow tiles: C tiles of 16 kRG rows x 16 kVec columns
+// (32x64, 16x64 or 16x32) on v_mfma_f32_16x16x4f32, for products too small
+// or too thin to fill the chip
 // with the ring body's 128x128 and 256x256 tiles (M <= 16, where B is read
 // once and HBM is the bound; and products of a few million outputs or
 // fewer, where small tiles give every CU a share without deep K splits).
@@ -30,10 +31,10 @@
 // (summed afterwards in range order, the epilogue applied there).
 //
 // Requirements (checked by the host): k and k_split multiples of 16, n a
-// multiple of kVec (the host asks for 4), A and B 16-byte aligned (C and the partials may be at
-// any float address). Rows past m read
-// row m - 1 and columns past n the last column chunk (every load in
-// bounds); what they produce is not stored.
+// multiple of kVec (the host asks for 4), A and B 16-byte aligned (C and
+// the partials may be at any float address). Rows past m read row m - 1 and
+// columns past n the last column chunk (every load in bounds); what they
+// produce is not stored.
 #pragma once
 
 typedef float mc_nw_f32x4 __attribute__((ext_vector_type(4)));

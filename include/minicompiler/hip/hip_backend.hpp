@@ -100,6 +100,17 @@ struct HipOptions {
     // when set. Different split counts round differently (within the FP32
     // GEMM bound); the tile configuration does not change the bits.
     bool autotune = false;
+    // split_k matmuls on the ring or narrow FP32 bodies add their K splits'
+    // partials inside the GEMM launch: the last block to finish a split of a
+    // C tile adds the tile's partials in split order (the same bits as the
+    // separate sum) and stores C through any fused epilogue; per-tile arrival
+    // counters live in the arena, zeroed once at compile time. Off (the
+    // default): a separate sum launch, as the C ABI's mc_launch_matmul does.
+    // Measured on an MI355X (graph-timed, operands past the MALL), the fold
+    // is the slower: 16x4096x4096 18.0 us against 17.0, 256x256x16384 30.5
+    // against 28.1, 1024^3 61 against 28 (one CU per tile reads the tile's
+    // partials with device-scope loads, at memory latency).
+    bool split_fold = false;
     // The FP32 ring tile configuration of double_buffered / split_k matmuls
     // without autotune (MCHIP_RING_*: 0 the planner's own, 1 wide 128x128,
     // 2 mid 64x128, 3 big 256x256, 4 thin 32x128). Same bits as the planner's.

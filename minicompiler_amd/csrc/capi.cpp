@@ -127,6 +127,8 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             o.graph_replay = value != "0" && value != "false";
         } else if (key == "autotune") {
             o.autotune = value != "0" && value != "false";
+        } else if (key == "split_fold") {
+            o.split_fold = value != "0" && value != "false";
         } else if (key == "ring") {
             static const char* const names[] = {"auto", "wide", "mid", "big", "thin", "narrow"};
             int cfg = -1;
@@ -141,8 +143,8 @@ Result<hip::HipOptions> parse_options(const char* spec) {
             o.nontemporal_stores = value != "0" && value != "false";
         } else {
             return Error{"unknown option '" + key +
-                         "' (matmul, vectorize, device, epilogue, graph, autotune, ring, tc_convert, ew_items, "
-                         "ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
+                         "' (matmul, vectorize, device, epilogue, graph, autotune, split_fold, ring, tc_convert, "
+                         "ew_items, ew_nt_loads, ew_nt_stores, ew_blocks_per_cu)"};
         }
     }
     return o;

@@ -112,16 +112,20 @@ Status hip_status(int rc, const char* what) {
         if (!st_.ok()) return st_.error();                  \
     } while (0)
 
-Result<Fp32Choice> time_candidates(int m, int n, int k, const std::vector<Fp32Choice>& cands) {
+Result<Fp32Choice> time_candidates(int m, int n, int k, const std::vector<Fp32Choice>& cands, bool fold) {
     const std::size_t mn = static_cast<std::size_t>(m) * n;
     int max_split = 1;
     for (const Fp32Choice& c : cands) max_split = std::max(max_split, c.splits);
-    DeviceMem a, b, c, ws;
+    DeviceMem a, b, c, ws, counters;
     Resources r;
     MC_AT_TRY(mchip_malloc(&a.p, static_cast<std::size_t>(m) * k * 4));
     MC_AT_TRY(mchip_malloc(&b.p, static_cast<std::size_t>(k) * n * 4));
     MC_AT_TRY(mchip_malloc(&c.p, mn * 4));
     if (max_split > 1) MC_AT_TRY(mchip_malloc(&ws.p, static_cast<std::size_t>(max_split) * mn * 4));
+    const std::size_t counter_bytes = static_cast<std::size_t>(mchip_split_counter_bytes(m, n));
+    if (max_split > 1 && fold) {
+        MC_AT_TRY(mchip_malloc(&counters.p, counter_bytes));
+    }
     MC_AT_TRY(mchip_stream_create(&r.stream));
     MC_AT_TRY(mchip_event_create(&r.start));
     MC_AT_TRY(mchip_event_create(&r.stop));
@@ -129,13 +133,15 @@ Result<Fp32Choice> time_candidates(int m, int n, int k, const std::vector<Fp32Ch
     // the matrix units draw power, and the clock follows, by the data.
     MC_AT_TRY(mchip_memset_async(a.p, 0x3c, static_cast<std::size_t>(m) * k * 4, r.stream));
     MC_AT_TRY(mchip_memset_async(b.p, 0x3c, static_cast<std::size_t>(k) * n * 4, r.stream));
+    if (counters.p) MC_AT_TRY(mchip_memset_async(counters.p, 0, counter_bytes, r.stream));
 
     auto launch = [&](const Fp32Choice& ch) {
         const int s = ch.splits;
         const MatmulKernel kernel = s > 1 ? MatmulKernel::SplitK : MatmulKernel::DoubleBuffered;
-        return mchip_launch_matmul_cfg(static_cast<int>(kernel), static_cast<const float*>(a.p),
-                                       static_cast<const float*>(b.p), static_cast<float*>(c.p), m, n, k, r.stream, s,
-                                       s > 1 ? static_cast<float*>(ws.p) : nullptr, ch.ring_cfg);
+        return mchip_launch_matmul_fold(static_cast<int>(kernel), static_cast<const float*>(a.p),
+                                        static_cast<const float*>(b.p), static_cast<float*>(c.p), m, n, k, r.stream, s,
+                                        s > 1 ? static_cast<float*>(ws.p) : nullptr, ch.ring_cfg,
+                                        s > 1 ? static_cast<unsigned*>(counters.p) : nullptr);
     };
     auto time_reps = [&](const Fp32Choice& s, int reps, double* ms) -> Status {
         MC_AT_TRY(launch(s));
@@ -207,16 +213,16 @@ std::vector<Fp32Choice> autotune_candidates(int m, int n, int k, int cu_count) {
     return out;
 }
 
-Result<Fp32Choice> autotune_fp32(const DeviceInfo& device, int m, int n, int k) {
+Result<Fp32Choice> autotune_fp32(const DeviceInfo& device, int m, int n, int k, bool fold) {
     const std::vector<Fp32Choice> cands = autotune_candidates(m, n, k, device.cu_count);
     if (cands.size() == 1) return cands[0];
-    const std::string tag = device_tag(device);
+    const std::string tag = device_tag(device) + (fold ? "_fold" : "");
     Decisions& d = decisions();
     std::lock_guard<std::mutex> lock(d.mu);
     load_file(d, tag, device.cu_count);
     const Key key{tag, m, n, k};
     if (auto it = d.choice.find(key); it != d.choice.end()) return it->second;
-    Result<Fp32Choice> chosen = time_candidates(m, n, k, cands);
+    Result<Fp32Choice> chosen = time_candidates(m, n, k, cands, fold);
     if (!chosen.ok()) return chosen.error();
     d.choice[key] = chosen.value();
     append_file(tag, m, n, k, chosen.value());

@@ -38,10 +38,13 @@ std::vector<Fp32Choice> autotune_candidates(int m, int n, int k, int cu_count);
 // The fastest candidate for an FP32 matmul m x n x k on the current device
 // (`device` names it in the cache key), timed with the ahead-of-time kernels
 // on scratch operands; another candidate replaces the default only when more
-// than 2% faster. Results of different split counts differ in rounding only
-// (the partial sums are added in a fixed order), within the FP32 GEMM bound;
-// the configuration does not change the bits.
-Result<Fp32Choice> autotune_fp32(const DeviceInfo& device, int m, int n, int k);
+// than 2% faster. `fold`: split candidates add their partials in the GEMM
+// launch (mchip_launch_matmul_fold), as an executable with split_fold runs
+// them; those decisions are kept apart (tag suffix "_fold"). Results of
+// different split counts differ in rounding only (the partial sums are added
+// in a fixed order), within the FP32 GEMM bound; the configuration does not
+// change the bits.
+Result<Fp32Choice> autotune_fp32(const DeviceInfo& device, int m, int n, int k, bool fold = false);
 
 // Decisions held by this process (for tests and reports).
 std::size_t autotune_cached_decisions();

@@ -18,6 +18,8 @@
 
 #include "codegen.hpp"
 
+#include "rtc_sources.hpp"
+
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
@@ -249,6 +251,10 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
     os << "// minicompiler-hip " << (is_f32_body(body) ? "FP32" : body == GemmBody::Bf16Fast ? "bf16" : "fp16")
        << " GEMM with a fused epilogue: " << program.num_ops() << " op(s) on the result, out f32"
        << to_string(out_shape) << ".\n";
+    // The ring and narrow bodies add split-K partials in the launch through
+    // mc_split_last_arrival.
+    const bool folds = is_f32_body(body) && body != GemmBody::F32Mfma;
+    if (folds) os << kGemmSplitArrivalSource << "\n";
     os << gemm_body_source << "\n";
     os << program_function(program, num_inputs);
     // Index helpers of General inputs, in terms of the flat output index i.
@@ -301,21 +307,22 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
                                                                                        : "256, 2";
     os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
        << "(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n, int k, "
-          "int k_split, int depth, float* __restrict__ partial, McEpilogue epi)\n{\n"
-       << unused << (constant ? "\t(void)k_split;\n" : "") << "\t(void)depth;\n";
+          "int k_split, int depth, float* __restrict__ partial, unsigned* __restrict__ counters, McEpilogue epi)\n{\n"
+       << unused << (constant ? "\t(void)k_split;\n" : "") << "\t(void)depth;\n"
+       << (folds ? "" : "\t(void)counters;\n");
     if (body == GemmBody::F32Mfma) {
         os << "\tmc_gemm_f32_mfma<true, " << (vectorized_operands ? "true" : "false") << ">(a, b, c, " << mnk
            << ", " << (constant ? std::to_string(fixed.k_split) : std::string("k_split")) << ", partial, epi);\n}\n\n";
     } else if (is_narrow_body(body)) {
         os << "\tmc_gemm_f32_narrow<" << narrow_config(body) << ">(a, b, c, "
-           << mnk << ", " << split << ", partial, epi);\n}\n\n";
+           << mnk << ", " << split << ", partial, counters, epi);\n}\n\n";
     } else {
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"
                           : body == GemmBody::F32RingThin ? "McRingThin"
                           : body == GemmBody::F32RingMid  ? "McRingMid"
                                                           : "McRingWide";
         os << "\tmc_gemm_f32_ring<" << cfg << ">(a, b, c, "
-           << mnk << ", " << split << ", partial, epi);\n}\n\n";
+           << mnk << ", " << split << ", partial, counters, epi);\n}\n\n";
     }
     // Split K: the partial sums added in split order (a left fold from split
     // 0's value), then the epilogue. A lane issues `chunk` split loads before

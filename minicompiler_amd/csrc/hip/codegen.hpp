@@ -118,11 +118,14 @@ inline const char* narrow_config(GemmBody body) {
 // fused elementwise group that consumes the GEMM's result: the program's
 // input `acc_input` is the accumulated value; every other input is read at
 // the flat output index by its access class against `out_shape`. Kernel
-// arguments, FP32 bodies: (a, b, c, m, n, k, k_split, depth, partial, epi)
-// (two-stage: grid (N/128, M/128, depth) of 256 lanes; ring: the grid and
-// block of mchip_f32_ring_plan) and, for split K, (partial, c, count, depth,
-// epi); 16-bit bodies (one block of 512 lanes per 256x256 tile): (a, b, c,
-// m, n, k, epi). epi holds one float pointer per program
+// arguments, FP32 bodies: (a, b, c, m, n, k, k_split, depth, partial,
+// counters, epi) (two-stage: grid (N/128, M/128, depth) of 256 lanes; ring:
+// the grid and block of mchip_f32_ring_plan) and, for split K, the sum
+// kernel's (partial, c, count, depth, epi). With split K on a ring or narrow
+// body and `counters` not null (one zeroed unsigned per tile), the GEMM
+// launch adds the partials itself and the sum kernel is not launched; the
+// two-stage body ignores counters. 16-bit bodies (one block of 512 lanes per
+// 256x256 tile): (a, b, c, m, n, k, epi). epi holds one float pointer per program
 // input (that of `acc_input` unused). `vectorized_operands` (FP32): A and B
 // rows allow 16-byte loads (k and n multiples of 4, 16-byte aligned).
 // The product's dimensions, when the kernel serves one shape only: the

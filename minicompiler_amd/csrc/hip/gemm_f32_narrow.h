@@ -5,8 +5,9 @@
 // once and HBM is the bound; and products of a few million outputs or
 // fewer, where small tiles give every CU a share without deep K splits).
 // Shared by the ahead-of-time kernels (identity epilogue) and the GEMMs
-// compiled at run time with a fused elementwise epilogue. Self-contained (no
-// headers), so hipRTC compiles it as is.
+// compiled at run time with a fused elementwise epilogue. No headers, so
+// hipRTC compiles it as is; it uses the split-K helpers
+// of gemm_split_arrival.h, which the includer puts before it.
 //
 // No LDS staging of operands: each wave loads its A and B fragments straight
 // from global memory (L2 for data other waves share) into registers, all the
@@ -27,12 +28,15 @@
 // col0 + V c + j, so accumulator (r, j) holds, in lane l, C[16 r + 4s + v]
 // [col0 + V c + j] for v = 0..3. The waves' tiles are then added in wave
 // order through LDS (a fixed order), and the block stores its tile to C
-// through the epilogue, or, with several K ranges, to its range's partial
-// (summed afterwards in range order, the epilogue applied there).
+// through the epilogue, or, with several K ranges, to its range's partial:
+// with `counters`, the last of the tile's blocks to finish then adds the
+// ranges' partials in range order and stores C through the epilogue
+// (mc_split_last_arrival); without, a separate launch adds them.
 //
 // Requirements (checked by the host): k and k_split multiples of 16, n a
 // multiple of kVec (the host asks for 4), A and B 16-byte aligned (C and
-// the partials may be at any float address). Rows past m read row m - 1 and
+// the partials may be at any float address; counters: one zeroed unsigned
+// per tile, in tile order). Rows past m read row m - 1 and
 // columns past n the last column chunk (every load in bounds); what they
 // produce is not stored.
 #pragma once
@@ -90,11 +94,13 @@ struct McNarrowRegs {
 
 // The tile of C at (row0, col0) and its K range [kb, ke), accumulated by
 // this block; the epilogue maps each value v of flat element i to what is
-// stored (out = C), or the raw sums go to `out` (a partial).
+// stored (out = C), or the raw sums go to `out` (a partial), added in the
+// launch when `counters` is given (not null).
 template <class Cfg, typename Epilogue>
 __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, const float* __restrict__ b,
                                                    float* __restrict__ c, int m, int n, int k, int k_split,
-                                                   int depth, float* __restrict__ partial, const Epilogue& epilogue) {
+                                                   int depth, float* __restrict__ partial, unsigned* __restrict__ counters,
+                                                   const Epilogue& epilogue) {
     constexpr int kRG = Cfg::kRG, kW = Cfg::kW, kVec = Cfg::kVec, kU = Cfg::kU;
     typedef typename McNarrowVec<kVec>::type BV;
     __shared__ BV red[kW][Cfg::kRows][16];  // [wave][row][column chunk]
@@ -217,7 +223,9 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     const bool raw = depth > 1;
     float* __restrict__ out = raw ? partial + static_cast<long long>(by) * m * n : c;
     // C or a partial may sit at any 4-byte address (a caller's workspace):
-    // then a chunk is stored float by float, the same values.
+    // then a chunk is stored float by float, the same values. Partials that
+    // this launch adds go out as device-scope stores (mc_split_store).
+    const bool fold = raw && counters != nullptr;
     const bool vec_out = (reinterpret_cast<unsigned long long>(out) & (sizeof(BV) - 1)) == 0;
     for (int t = threadIdx.x; t < Cfg::kRows * 16; t += Cfg::kThreads) {
         const int r = t >> 4, ch = t & 15;
@@ -231,12 +239,54 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
 #pragma unroll
                 for (int j = 0; j < kVec; ++j) sum[j] = epilogue(sum[j], static_cast<unsigned>(at + j));
             }
-            if (vec_out) {
+            if (fold) {
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) mc_split_store(out + at + j, sum[j]);
+            } else if (vec_out) {
                 *reinterpret_cast<BV*>(out + at) = sum;
             } else {
 #pragma unroll
                 for (int j = 0; j < kVec; ++j) out[at + j] = sum[j];
             }
+        }
+    }
+    if (!fold) return;
+
+    // The last block of the tile adds the ranges' partials, range 0 first (a
+    // lane issues its loads of 8 ranges before it adds them), and stores C.
+    __shared__ int last_flag;
+    if (!mc_split_last_arrival(counters + bz * tiles_n + bx, depth, &last_flag)) return;
+    const long long plane = static_cast<long long>(m) * n;
+    const bool vec_c = (reinterpret_cast<unsigned long long>(c) & (sizeof(BV) - 1)) == 0;
+    constexpr int kChunk = 8;
+    for (int t = threadIdx.x; t < Cfg::kRows * 16; t += Cfg::kThreads) {
+        const int r = t >> 4, ch = t & 15;
+        const int row = row0 + r, col = col0 + kVec * ch;
+        if (row >= m || col >= n) continue;
+        const long long at = static_cast<long long>(row) * n + col;
+        auto load = [&](int z) {
+            const float* p = partial + z * plane + at;
+            BV x;
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) x[j] = mc_split_load(p + j);
+            return x;
+        };
+        BV sum = load(0);
+        for (int z0 = 1; z0 < depth; z0 += kChunk) {
+            BV x[kChunk];
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) x[i] = load(z0 + i < depth ? z0 + i : depth - 1);
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i)
+                if (z0 + i < depth) sum += x[i];
+        }
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) sum[j] = epilogue(sum[j], static_cast<unsigned>(at + j));
+        if (vec_c) {
+            *reinterpret_cast<BV*>(c + at) = sum;
+        } else {
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) c[at + j] = sum[j];
         }
     }
 }

@@ -2,8 +2,9 @@
 // ring fed by direct global -> LDS loads and persistent blocks that walk
 // their tiles in sequence. Shared by the ahead-of-time kernels
 // (matmul_fp32.hip, identity epilogue) and the GEMMs compiled at run time
-// with a fused elementwise epilogue. Self-contained: no standard or HIP
-// headers, so hipRTC compiles it as is.
+// with a fused elementwise epilogue. No standard or HIP headers, so hipRTC
+// compiles it as is; it uses the split-K helpers of gemm_split_arrival.h,
+// which the includer puts before it.
 //
 // Same arithmetic as the two-stage body in gemm_f32_mfma.h: each C element
 // is accumulated by the same v_mfma_f32_32x32x2_f32 sequence (the 32-wide K
@@ -12,7 +13,8 @@
 // serve a request they all accept.
 //
 // Requirements (checked by the host): K (and the split size) a multiple of
-// 32, N a multiple of 4, A, B and C 16-byte aligned, every split non-empty.
+// 32, N a multiple of 4, A, B, C and the partials 16-byte aligned, every
+// split non-empty; counters (when given): one zeroed unsigned per tile.
 // Rows past M and columns past N are clamped to the last row / column
 // chunk, so every load is in bounds; what they bring only reaches C elements
 // that are not stored.
@@ -305,7 +307,9 @@ __device__ __forceinline__ void mc_ring_barrier() {
 // the latter). kCheck: some rows may be past M. Without it the store is
 // straight-line code, so the compiler can issue the epilogue's operand loads
 // for many rows before the first store instead of one row at a time.
-template <class Cfg, bool kCheck, typename Epilogue>
+// kSplit: raw partial sums that this launch adds, stored float by float
+// with device-scope stores (mc_split_store).
+template <class Cfg, bool kCheck, typename Epilogue, bool kSplit = false>
 __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ], float* __restrict__ out,
                                               int row0, int col, int m, int n, bool raw, const Epilogue& epilogue) {
     typedef McRingVec<Cfg::kBJ> BV;
@@ -316,6 +320,11 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
             const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
             if (kCheck && row >= m) continue;
             const long long at = static_cast<long long>(row) * n + col;
+            if constexpr (kSplit) {
+#pragma unroll
+                for (int j = 0; j < Cfg::kBJ; ++j) mc_split_store(out + at + j, acc[i][j][v]);
+                continue;
+            }
             typename BV::type o;
 #pragma unroll
             for (int j = 0; j < Cfg::kBJ; ++j) {
@@ -324,6 +333,37 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
             }
             *reinterpret_cast<typename BV::type*>(out + at) = o;
         }
+    }
+}
+
+// C tile (row0, col0) from the partials of its `splits` K splits, added in
+// split order (a lane issues its loads of 8 splits before it adds them) and
+// stored through the epilogue, 16 bytes per lane and step.
+template <class Cfg, typename Epilogue>
+__device__ __forceinline__ void mc_ring_fold(const float* __restrict__ partial, float* __restrict__ c, int row0,
+                                             int col0, int m, int n, int splits, const Epilogue& epilogue) {
+    constexpr int kQ = Cfg::kBN / 4, kChunk = 8;
+    const long long plane = static_cast<long long>(m) * n;
+    for (int t = threadIdx.x; t < Cfg::kBM * kQ; t += Cfg::kThreads) {
+        const int row = row0 + t / kQ, col = col0 + 4 * (t % kQ);
+        if (row >= m || col >= n) continue;
+        const long long at = static_cast<long long>(row) * n + col;
+        auto load = [&](int z) {
+            const float* p = partial + z * plane + at;
+            return mc_ring_f32x4{mc_split_load(p), mc_split_load(p + 1), mc_split_load(p + 2), mc_split_load(p + 3)};
+        };
+        mc_ring_f32x4 sum = load(0);
+        for (int z0 = 1; z0 < splits; z0 += kChunk) {
+            mc_ring_f32x4 x[kChunk];
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) x[i] = load(z0 + i < splits ? z0 + i : splits - 1);
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i)
+                if (z0 + i < splits) sum += x[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum[j] = epilogue(sum[j], static_cast<unsigned>(at + j));
+        *reinterpret_cast<mc_ring_f32x4*>(c + at) = sum;
     }
 }
 
@@ -336,11 +376,13 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
 // With one split the epilogue maps each accumulated value v of element
 // i = row n + col to what is stored; with several, the raw partial sums go
 // to `partial` (split s at s m n) and the epilogue is applied where the
-// splits are summed.
+// splits are summed: in this launch, by the last block to finish a split of
+// the tile, when `counters` is given (not null), else by a separate launch.
 template <class Cfg, typename Epilogue>
 __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, const float* __restrict__ b,
                                                  float* __restrict__ c, int m, int n, int k, int k_split, int splits,
-                                                 float* __restrict__ partial, const Epilogue& epilogue) {
+                                                 float* __restrict__ partial, unsigned* __restrict__ counters,
+                                                 const Epilogue& epilogue) {
     typedef McRingVec<Cfg::kBJ> BV;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[Cfg::kLds];
     MC_RING_LDS unsigned char* lds = (MC_RING_LDS unsigned char*)(smem);  // generic -> LDS address space
@@ -499,12 +541,27 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
         }
 
         const int col = u.col0 + lcol;
-        if (col >= n) continue;
-        float* __restrict__ out = splits > 1 ? partial + static_cast<long long>(u.split) * m * n : c;
-        if (u.row0 + Cfg::kBM <= m)
-            mc_ring_store<Cfg, false>(acc, out, u.row0 + wr + 4 * half, col, m, n, splits > 1, epilogue);
-        else
-            mc_ring_store<Cfg, true>(acc, out, u.row0 + wr + 4 * half, col, m, n, splits > 1, epilogue);
+        const bool fold = splits > 1 && counters != nullptr;
+        if (col < n) {
+            float* __restrict__ out = splits > 1 ? partial + static_cast<long long>(u.split) * m * n : c;
+            const int r0 = u.row0 + wr + 4 * half;
+            if (fold) {
+                if (u.row0 + Cfg::kBM <= m)
+                    mc_ring_store<Cfg, false, Epilogue, true>(acc, out, r0, col, m, n, true, epilogue);
+                else
+                    mc_ring_store<Cfg, true, Epilogue, true>(acc, out, r0, col, m, n, true, epilogue);
+            } else if (u.row0 + Cfg::kBM <= m) {
+                mc_ring_store<Cfg, false>(acc, out, r0, col, m, n, splits > 1, epilogue);
+            } else {
+                mc_ring_store<Cfg, true>(acc, out, r0, col, m, n, splits > 1, epilogue);
+            }
+        }
+        if (fold) {
+            __shared__ int last_flag;
+            const int tile = (u.row0 / Cfg::kBM) * tiles_n + u.col0 / Cfg::kBN;
+            if (mc_split_last_arrival(counters + tile, splits, &last_flag))
+                mc_ring_fold<Cfg>(partial, c, u.row0, u.col0, m, n, splits, epilogue);
+        }
     }
     MC_RING_WAIT(0);
 }

@@ -69,6 +69,10 @@ struct Launch {
     int splits = 1;
     int ring_cfg = 0;  // MCHIP_RING_*: forced FP32 ring configuration (0: the planner's)
     float* workspace = nullptr;
+    // split_k: per-tile arrival counters (zeroed at init) when the GEMM
+    // launch adds its splits' partials itself (split_fold), else null.
+    unsigned* counters = nullptr;
+    bool fold = false;  // FusedMatmul: the generated GEMM adds the partials (no sum launch)
     int m = 0, n = 0, k = 0;
     // FusedMatmul: generated kernels and their stable arguments.
     void* sum_function = nullptr;
@@ -142,8 +146,8 @@ public:
             }
         }
 
-        // Launches (matmul workspaces take arena space too).
-        std::vector<std::size_t> workspace_offset;
+        // Launches (matmul workspaces and split counters take arena space too).
+        std::vector<std::size_t> workspace_offset, counter_offset;
         std::vector<bool> fused_away(n, false);
         for (std::size_t i = 0; i < n; ++i) {
             const auto id = static_cast<NodeId>(i);
@@ -173,9 +177,15 @@ public:
                            : matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
                 workspace_offset.push_back(ws ? top : SIZE_MAX);
                 if (ws) top += align_up(ws);
+                const std::size_t cb = ws && !l.lowp && options_.split_fold && l.matmul == MatmulKernel::SplitK
+                                           ? static_cast<std::size_t>(mchip_split_counter_bytes(l.m, l.n))
+                                           : 0;
+                counter_offset.push_back(cb ? top : SIZE_MAX);
+                if (cb) top += align_up(cb);
             } else {
                 l.kind = Launch::Kind::Elementwise;
                 workspace_offset.push_back(SIZE_MAX);
+                counter_offset.push_back(SIZE_MAX);
             }
             launches_.push_back(std::move(l));
         }
@@ -190,6 +200,11 @@ public:
                 l.b16 = base + workspace_offset[j] + align_up(static_cast<std::size_t>(l.m) * l.k * 2);
             } else {
                 l.workspace = reinterpret_cast<float*>(base + workspace_offset[j]);
+            }
+            if (counter_offset[j] != SIZE_MAX) {
+                l.counters = reinterpret_cast<unsigned*>(base + counter_offset[j]);
+                MCHIP_TRY(mchip_memset_async(l.counters, 0, static_cast<std::size_t>(mchip_split_counter_bytes(l.m, l.n)),
+                                             stream_));
             }
         }
         // Constants are uploaded once, here.
@@ -382,6 +397,7 @@ public:
                 std::string name = std::string("matmul ") + matmul_kernel_name(l.matmul) + " " + std::to_string(l.m) +
                                    "x" + std::to_string(l.n) + "x" + std::to_string(l.k) +
                                    (l.splits > 1 ? " splits=" + std::to_string(l.splits) : "");
+                if (folds(l)) name += ", summed in the GEMM";
                 if (l.kind == Launch::Kind::FusedMatmul) {
                     const Node& f = graph_.node(l.epilogue_node);
                     name += " + fused " + f.name + " " + to_string(f.type);
@@ -443,7 +459,7 @@ private:
         if (l.kind == Launch::Kind::FusedMatmul) {
             int rc = mchip_module_launch3(l.function, l.grid_x, l.grid_y, l.grid_z, l.block, 0, s, l.params.data());
             if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
-            if (l.depth > 1) {
+            if (l.depth > 1 && !l.fold) {
                 rc = mchip_module_launch(l.sum_function, l.sum_grid, 256, 0, s, l.sum_params.data());
                 if (rc != 0) return hip_status(rc, "hipModuleLaunchKernel(mc_sum_splits_epilogue)");
             }
@@ -456,13 +472,21 @@ private:
         // caller buffers may not be); the planner's own choice runs any.
         const bool aligned = ((reinterpret_cast<std::uintptr_t>(pa) | reinterpret_cast<std::uintptr_t>(pb) |
                                reinterpret_cast<std::uintptr_t>(pc)) & 15u) == 0;
-        const int rc = mchip_launch_matmul_cfg(static_cast<int>(l.matmul), static_cast<const float*>(pa),
-                                               static_cast<const float*>(pb), static_cast<float*>(pc), l.m, l.n, l.k,
-                                               s, l.splits, l.workspace, aligned ? l.ring_cfg : 0);
+        const int rc = mchip_launch_matmul_fold(static_cast<int>(l.matmul), static_cast<const float*>(pa),
+                                                static_cast<const float*>(pb), static_cast<float*>(pc), l.m, l.n, l.k,
+                                                s, l.splits, l.workspace, aligned ? l.ring_cfg : 0, l.counters);
         if (rc != 0) {
             return Error{std::string("launch_matmul(") + matmul_kernel_name(l.matmul) + "): " + mchip_error_string(rc)};
         }
         return Status();
+    }
+
+    // Whether the launch adds its K splits' partials itself (no sum launch),
+    // for 16-byte aligned operands (arena buffers always are).
+    bool folds(const Launch& l) const {
+        if (l.kind == Launch::Kind::FusedMatmul) return l.fold;
+        return l.kind == Launch::Kind::Matmul && l.counters != nullptr &&
+               mchip_split_k_folds(l.m, l.n, l.k, l.splits, l.ring_cfg) != 0;
     }
 
     // The captured graph holds the kernel arguments of the time of capture.
@@ -504,7 +528,7 @@ private:
             // The split count and ring configuration timed on this device
             // (double_buffered unsplit, split_k otherwise) instead of the
             // split rule's count and the planner's configuration.
-            Result<Fp32Choice> tuned = autotune_fp32(device_, l->m, l->n, l->k);
+            Result<Fp32Choice> tuned = autotune_fp32(device_, l->m, l->n, l->k, options_.split_fold);
             if (!tuned.ok()) return tuned.error();
             l->splits = tuned->splits;
             l->ring_cfg = tuned->ring_cfg;
@@ -712,6 +736,8 @@ private:
                 l.sum_grid = static_cast<unsigned>(std::max<std::size_t>(
                     1, std::min<std::size_t>((static_cast<std::size_t>(l.count) + 255) / 256, 8192)));
                 l.partial = l.depth > 1 ? l.workspace : nullptr;
+                l.fold = l.depth > 1 && l.counters != nullptr && l.body != GemmBody::F32Mfma;
+                if (!l.fold) l.counters = nullptr;
                 l.epilogue_inputs.assign(graph_.node(l.epilogue_node).inputs.size(), nullptr);
                 continue;
             }
@@ -741,7 +767,7 @@ private:
             }
             if (l.kind == Launch::Kind::FusedMatmul) {
                 l.params = {&l.a_ptr, &l.b_ptr, &l.c_ptr, &l.m, &l.n, &l.k, &l.k_split, &l.depth, &l.partial,
-                            l.epilogue_inputs.data()};
+                            &l.counters, l.epilogue_inputs.data()};
                 l.sum_params = {&l.partial, &l.c_ptr, &l.count, &l.depth, l.epilogue_inputs.data()};
                 continue;
             }

@@ -114,6 +114,22 @@ int mchip_launch_narrow(const float* a, const float* b, float* c, int m, int n, 
 int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
                             int splits, float* workspace, int ring_cfg);
 
+/* mchip_launch_matmul_cfg for split_k that adds the K splits' partials in
+ * the GEMM launch itself where the ring or narrow body runs the product: the
+ * last block to finish a split of a C tile adds the tile's partials in split
+ * order (the bits of the separate sum) and stores C; no sum launch.
+ * `counters`: mchip_split_counter_bytes(m, n) bytes of device memory, zero
+ * before the first launch and left zero by every launch; launches that share
+ * them must not overlap. Other kernels, or counters null: as
+ * mchip_launch_matmul_cfg. */
+unsigned long long mchip_split_counter_bytes(int m, int n);
+/* 1 when mchip_launch_matmul_fold with counters adds the partials of this
+ * split_k product (16-byte aligned operands and workspace) in the GEMM
+ * launch: the plan runs it on the ring or narrow body in several K splits. */
+int mchip_split_k_folds(int m, int n, int k, int splits, int ring_cfg);
+int mchip_launch_matmul_fold(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
+                             int splits, float* workspace, int ring_cfg, unsigned* counters);
+
 /* mchip_launch_matmul with the split-K partials in the library's per-device
  * scratch array (matmul_noalloc.hip) instead of a caller workspace; no
  * device memory is allocated. hipErrorInvalidValue when the partials

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include "gemm_f32_mfma.h"
+#include "gemm_split_arrival.h"
 #include "gemm_f32_ring.h"
 #include "gemm_f32_narrow.h"
 
@@ -165,8 +166,8 @@ constexpr int kRBKRing = RingWide::kBK;
 template <class Cfg, int kBlocksPerCu>
 __global__ void __launch_bounds__(Cfg::kThreads, kBlocksPerCu)
     matmul_ring_f32(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ c, int m, int n,
-                    int k, int k_split, int depth, float* __restrict__ partial) {
-    mc_gemm_f32_ring<Cfg>(a, b, c, m, n, k, k_split, depth, partial, McGemmStore{});
+                    int k, int k_split, int depth, float* __restrict__ partial, unsigned* __restrict__ counters) {
+    mc_gemm_f32_ring<Cfg>(a, b, c, m, n, k, k_split, depth, partial, counters, McGemmStore{});
 }
 
 // ---------------------------------------------------------------- narrow tiles
@@ -179,8 +180,9 @@ template <class Cfg>
 __global__ void __launch_bounds__(Cfg::kThreads) matmul_narrow_f32(const float* __restrict__ a,
                                                                     const float* __restrict__ b, float* __restrict__ c,
                                                                     int m, int n, int k, int k_split, int depth,
-                                                                    float* __restrict__ partial) {
-    mc_gemm_f32_narrow<Cfg>(a, b, c, m, n, k, k_split, depth, partial, McIdentity{});
+                                                                    float* __restrict__ partial,
+                                                                    unsigned* __restrict__ counters) {
+    mc_gemm_f32_narrow<Cfg>(a, b, c, m, n, k, k_split, depth, partial, counters, McIdentity{});
 }
 
 // ---------------------------------------------------------------- split-K sum
@@ -238,77 +240,124 @@ int device_cu_count() {
 
 template <class Cfg>
 void narrow_kernel(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int k_split,
-                   int depth, float* part) {
+                   int depth, float* part, unsigned* counters) {
     const dim3 grid(((n + Cfg::kCols - 1) / Cfg::kCols) * depth * ((m + Cfg::kRows - 1) / Cfg::kRows));
     hipLaunchKernelGGL((matmul_narrow_f32<Cfg>), grid, dim3(Cfg::kThreads), 0, s, a, b, c, m, n, k, k_split, depth,
-                       part);
+                       part, counters);
 }
 
 // The narrow-tile body in tile shape `shape` on `depth` K ranges of
-// k_split, the partials summed in range order when there are several.
+// k_split, the partials summed in range order when there are several: in
+// the launch when `counters` (zeroed, one per tile) is given, else by a
+// separate launch.
 int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k, hipStream_t s, int shape,
-                  int k_split, int depth, float* workspace) {
+                  int k_split, int depth, float* workspace, unsigned* counters) {
     float* dst = depth > 1 ? workspace : c;
     if (!aligned16(a) || !aligned16(b) || dst == nullptr) return hipErrorInvalidValue;
     if (shape == MCHIP_NARROW_16X64_STREAM && m > 16) return hipErrorInvalidValue;
     float* part = depth > 1 ? workspace : nullptr;
+    unsigned* ctr = depth > 1 ? counters : nullptr;
     switch (shape) {
-        case MCHIP_NARROW_32X64: narrow_kernel<McNarrow32>(a, b, c, m, n, k, s, k_split, depth, part); break;
-        case MCHIP_NARROW_16X64_STREAM: narrow_kernel<McNarrow16>(a, b, c, m, n, k, s, k_split, depth, part); break;
-        case MCHIP_NARROW_16X64: narrow_kernel<McNarrow16x64>(a, b, c, m, n, k, s, k_split, depth, part); break;
-        case MCHIP_NARROW_16X32: narrow_kernel<McNarrow16x32>(a, b, c, m, n, k, s, k_split, depth, part); break;
+        case MCHIP_NARROW_32X64: narrow_kernel<McNarrow32>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
+        case MCHIP_NARROW_16X64_STREAM: narrow_kernel<McNarrow16>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
+        case MCHIP_NARROW_16X64: narrow_kernel<McNarrow16x64>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
+        case MCHIP_NARROW_16X32: narrow_kernel<McNarrow16x32>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
         default: return hipErrorInvalidValue;
     }
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || depth == 1) return e;
+    if (e != hipSuccess || depth == 1 || ctr != nullptr) return e;
     return mchip_sum_split_partials(workspace, c, static_cast<std::size_t>(m) * n, depth, s);
 }
 
-int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
-                    hipStream_t stream, int splits, float* workspace, int ring_cfg, bool split_k) {
+// How launch_mfma_f32 runs a product: the body (narrow tiles, a ring
+// configuration, or the two-stage body), its K ranges and grid. `a16`...:
+// whether A, B, C and the workspace are 16-byte aligned.
+struct MfmaPlan {
+    int status = hipSuccess;
+    bool narrow = false;
+    int shape = 0;  // MCHIP_NARROW_* when narrow
+    int ring = MCHIP_RING_NONE;
+    int k_split = 0, depth = 1;
+    unsigned ring_grid = 0, ring_block = 0;
+    bool vec = false;
+    // The split's partials go to a workspace and a body that can add them
+    // in its own launch (ring or narrow) runs it.
+    bool can_fold() const { return status == hipSuccess && depth > 1 && (narrow || ring != MCHIP_RING_NONE); }
+};
+
+MfmaPlan plan_mfma_f32(bool double_buffer, bool a16, bool b16, bool c16, bool ws16, bool has_ws, int m, int n, int k,
+                       int splits, int ring_cfg, bool split_k) {
+    MfmaPlan p;
     // split_k on the narrow-tile body when the plan (or the caller) takes it,
     // with at most the caller's split count (its workspace's size).
-    if (split_k && (ring_cfg == MCHIP_RING_NONE || ring_cfg == MCHIP_RING_NARROW) && aligned16(a) && aligned16(b)) {
+    if (split_k && (ring_cfg == MCHIP_RING_NONE || ring_cfg == MCHIP_RING_NARROW) && a16 && b16) {
         int shape = 0, ns = 0, nk = 0;
         if (mchip_f32_narrow_plan(m, n, k, std::max(splits, 1), device_cu_count(), ring_cfg == MCHIP_RING_NARROW,
                                   &shape, &ns, &nk)) {
-            if (ns > 1 && workspace == nullptr) return hipErrorInvalidValue;  // as the ring would
-            return launch_narrow(a, b, c, m, n, k, stream, shape, nk, ns, workspace);
+            p.narrow = true;
+            p.shape = shape;
+            p.k_split = nk;
+            p.depth = ns;
+            if (ns > 1 && !has_ws) p.status = hipErrorInvalidValue;  // as the ring would
+            return p;
         }
     }
-    if (ring_cfg == MCHIP_RING_NARROW) return hipErrorInvalidValue;
-    if (split_k && ring_cfg == MCHIP_RING_NONE && aligned16(a) && aligned16(b) && aligned16(c) &&
+    if (ring_cfg == MCHIP_RING_NARROW) {
+        p.status = hipErrorInvalidValue;
+        return p;
+    }
+    if (split_k && ring_cfg == MCHIP_RING_NONE && a16 && b16 && c16 &&
         mchip_f32_unsplit_ring(m, n, k, splits, device_cu_count())) {
         splits = 1;
         ring_cfg = MCHIP_RING_MID;
     }
-    const int k_split = split_len(k, splits, kMBK);
-    const int depth = std::max(1, (k + k_split - 1) / k_split);
-    if (depth > 1 && workspace == nullptr) return hipErrorInvalidValue;
-    const dim3 grid((n + kMBN - 1) / kMBN, (m + kMBM - 1) / kMBM, depth);
-    const bool vec = n % 4 == 0 && k % 4 == 0 && aligned16(a) && aligned16(b);
-    float* out_ws = depth > 1 ? workspace : nullptr;
-    unsigned ring_grid = 0, ring_block = 0;
+    p.k_split = split_len(k, splits, kMBK);
+    p.depth = std::max(1, (k + p.k_split - 1) / p.k_split);
+    if (p.depth > 1 && !has_ws) {
+        p.status = hipErrorInvalidValue;
+        return p;
+    }
+    p.vec = n % 4 == 0 && k % 4 == 0 && a16 && b16;
     // The ring body stores C (or a split's partial) 4, 8 or 16 bytes at a
     // time: the destination must be 16-byte aligned, as the reference
     // requires of the workspace (matmul_kernels.cu:324).
-    const bool dest_aligned = depth > 1 ? aligned16(workspace) : aligned16(c);
-    const int ring = double_buffer && vec && dest_aligned
-                         ? mchip_f32_ring_plan_cfg(m, n, k, depth, device_cu_count(), ring_cfg, &ring_grid, &ring_block)
-                         : MCHIP_RING_NONE;
-    if (ring_cfg != MCHIP_RING_NONE && ring != ring_cfg) return hipErrorInvalidValue;
+    const bool dest_aligned = p.depth > 1 ? ws16 : c16;
+    p.ring = double_buffer && p.vec && dest_aligned
+                 ? mchip_f32_ring_plan_cfg(m, n, k, p.depth, device_cu_count(), ring_cfg, &p.ring_grid, &p.ring_block)
+                 : MCHIP_RING_NONE;
+    if (ring_cfg != MCHIP_RING_NONE && p.ring != ring_cfg) p.status = hipErrorInvalidValue;
+    return p;
+}
+
+// `counters` (zeroed, one per tile; may be null): where the ring or narrow
+// body runs the split, the launch adds the partials itself.
+int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c, int m, int n, int k,
+                    hipStream_t stream, int splits, float* workspace, int ring_cfg, bool split_k,
+                    unsigned* counters = nullptr) {
+    const MfmaPlan p = plan_mfma_f32(double_buffer, aligned16(a), aligned16(b), aligned16(c), aligned16(workspace),
+                                     workspace != nullptr, m, n, k, splits, ring_cfg, split_k);
+    if (p.status != hipSuccess) return p.status;
+    if (p.narrow) return launch_narrow(a, b, c, m, n, k, stream, p.shape, p.k_split, p.depth, workspace, counters);
+    const int k_split = p.k_split, depth = p.depth;
+    const dim3 grid((n + kMBN - 1) / kMBN, (m + kMBM - 1) / kMBM, depth);
+    const bool vec = p.vec;
+    float* out_ws = depth > 1 ? workspace : nullptr;
+    const unsigned ring_grid = p.ring_grid, ring_block = p.ring_block;
+    const int ring = p.ring;
+    // The ring's fold stores C 16 bytes at a time.
+    unsigned* ctr = p.can_fold() && aligned16(c) ? counters : nullptr;
     if (ring == MCHIP_RING_THIN) {
         hipLaunchKernelGGL((matmul_ring_f32<RingThin, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
-                           k, k_split, depth, out_ws);
+                           k, k_split, depth, out_ws, ctr);
     } else if (ring == MCHIP_RING_BIG) {
         hipLaunchKernelGGL((matmul_ring_f32<RingBig, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
-                           k, k_split, depth, out_ws);
+                           k, k_split, depth, out_ws, ctr);
     } else if (ring == MCHIP_RING_WIDE) {
         hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
-                           k, k_split, depth, out_ws);
+                           k, k_split, depth, out_ws, ctr);
     } else if (ring == MCHIP_RING_MID) {
         hipLaunchKernelGGL((matmul_ring_f32<RingMid, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
-                           k, k_split, depth, out_ws);
+                           k, k_split, depth, out_ws, ctr);
     } else if (double_buffer) {
         if (vec) {
             hipLaunchKernelGGL((matmul_mfma_f32<true, true>), grid, dim3(256), 0, stream, a, b, c, m, n, k, k_split, out_ws);
@@ -323,7 +372,7 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
         }
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || depth == 1) return e;
+    if (e != hipSuccess || depth == 1 || ctr != nullptr) return e;
     return mchip_sum_split_partials(workspace, c, static_cast<std::size_t>(m) * n, depth, stream);
 }
 
@@ -460,7 +509,7 @@ extern "C" int mchip_launch_narrow(const float* a, const float* b, float* c, int
     const int k_split = ((k + splits - 1) / splits + 15) / 16 * 16;
     return launch_narrow(a, b, c, m, n, k, static_cast<hipStream_t>(stream),
                          rows == 16 ? MCHIP_NARROW_16X64_STREAM : MCHIP_NARROW_32X64, k_split,
-                         (k + k_split - 1) / k_split, workspace);
+                         (k + k_split - 1) / k_split, workspace, nullptr);
 }
 
 extern "C" int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
@@ -545,4 +594,25 @@ extern "C" int mchip_launch_matmul_cfg(int kernel, const float* a, const float* 
         case kSplitK: return launch_mfma_f32(true, a, b, c, m, n, k, s, splits, workspace, ring_cfg, true);
         default: return hipErrorInvalidValue;  // only the ring rungs take a configuration
     }
+}
+
+extern "C" unsigned long long mchip_split_counter_bytes(int m, int n) {
+    if (m < 1 || n < 1) return 0;
+    // The smallest tiles of any body that folds (16x32 narrow tiles).
+    return 4ull * ((static_cast<unsigned long long>(m) + 15) / 16) * ((static_cast<unsigned long long>(n) + 31) / 32);
+}
+
+extern "C" int mchip_split_k_folds(int m, int n, int k, int splits, int ring_cfg) {
+    if (m < 1 || n < 1 || k < 1) return 0;
+    return plan_mfma_f32(true, true, true, true, true, true, m, n, k, splits, ring_cfg, true).can_fold() ? 1 : 0;
+}
+
+extern "C" int mchip_launch_matmul_fold(int kernel, const float* a, const float* b, float* c, int m, int n, int k,
+                                        void* stream, int splits, float* workspace, int ring_cfg, unsigned* counters) {
+    if (kernel != kSplitK || counters == nullptr) {
+        return mchip_launch_matmul_cfg(kernel, a, b, c, m, n, k, stream, splits, workspace, ring_cfg);
+    }
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    return launch_mfma_f32(true, a, b, c, m, n, k, static_cast<hipStream_t>(stream), splits, workspace, ring_cfg, true,
+                           counters);
 }

@@ -62,7 +62,7 @@ struct McNarrowVec<2> {
 };
 
 // A configuration: kRG row groups of 16, kVec columns per lane and load
-// (tiles of 16 kVec columns), kW waves, kU groups of 16 k per batch of
+// (tiles of 16 kVec columns), kW waves, up to kU groups of 16 k per batch of
 // loads; kStreamB: B is read by one tile row only (M <= 16), so its loads
 // are non-temporal (a read-only stream reached 7.1 TB/s with them against
 // 6.3 TB/s without on an MI355X).
@@ -73,15 +73,15 @@ struct McNarrowCfg {
     static constexpr int kRows = 16 * kRG, kCols = 16 * kVec, kThreads = 64 * kW;
 };
 
-// The configurations the library runs, 4 waves each: 16x64 tiles for
-// M <= 16 (B streamed), 32x64 tiles, and for short-K products that these
-// would leave with half the CUs idle, 16x64 and 16x32 tiles (the latter
-// with batches of 2 groups). At one K range every configuration adds the
-// same products in the same order (per element: the 4 waves' pieces of K in
-// wave order, each a chain of 16x16x4 MFMAs), so they give the same bits.
-using McNarrow16 = McNarrowCfg<1, 4, 4, 4, true>;
-using McNarrow32 = McNarrowCfg<2, 4, 4, 4, false>;
-using McNarrow16x64 = McNarrowCfg<1, 4, 4, 4, false>;
+// The configurations the library runs, 4 waves each, batches of up to 2
+// groups: 16x64 tiles for M <= 16 (B streamed), 32x64 tiles, and for
+// short-K products that these would leave with half the CUs idle, 16x64 and
+// 16x32 tiles. At one K range every configuration adds the same products in
+// the same order (per element: the 4 waves' pieces of K in wave order, each
+// a chain of 16x16x4 MFMAs), so they give the same bits.
+using McNarrow16 = McNarrowCfg<1, 4, 4, 2, true>;
+using McNarrow32 = McNarrowCfg<2, 4, 4, 2, false>;
+using McNarrow16x64 = McNarrowCfg<1, 4, 4, 2, false>;
 using McNarrow16x32 = McNarrowCfg<1, 2, 4, 2, false>;
 
 // One batch of a wave's operands: kU groups of 16 k.
@@ -182,30 +182,44 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     // loads in flight while its matrix core works. Every load is issued
     // unconditionally where it is issued (the last batch is peeled off): a
     // load under a condition would make the compiler wait for all loads
-    // before the next MFMA.
-    const int batches = (g1 - g0) / kU;
+    // before the next MFMA. A batch is kU groups when each wave has 32 groups
+    // or more, else one group: a short piece gains more from MFMAs that start
+    // after one group's loads than from more loads in flight. Measured on an
+    // MI355X (batches of 1 / 2 / 4 groups): 256x2048x512 on 32x64 tiles 7.8 /
+    // 9.0 / 10.5 us, 512^3 on 16x64 tiles 5.0 / 5.2 / 6.1 us, 16x4096x4096
+    // streamed in 4 K ranges 13.4 / 13.9 / 14.4 us; 256x256x16384 on 32x64
+    // tiles in 8 ranges (32 groups per wave) 21.7 / 21.0 / 24.9 us. The
+    // batching does not change the order of the adds.
     McNarrowRegs<Cfg> x0, x1;
-    constexpr auto kBatch = McNarrowUnits<kU>{};
-    if (batches > 0) {
-        int i = 0;
-        load(x0, g0, kBatch);
-        for (; i + 2 < batches; i += 2) {
-            load(x1, g0 + (i + 1) * kU, kBatch);
-            compute(x0, kBatch);
-            load(x0, g0 + (i + 2) * kU, kBatch);
-            compute(x1, kBatch);
+    auto pipeline = [&](auto units) {
+        constexpr int kN = decltype(units)::value;
+        const int batches = (g1 - g0) / kN;
+        if (batches > 0) {
+            int i = 0;
+            load(x0, g0, units);
+            for (; i + 2 < batches; i += 2) {
+                load(x1, g0 + (i + 1) * kN, units);
+                compute(x0, units);
+                load(x0, g0 + (i + 2) * kN, units);
+                compute(x1, units);
+            }
+            if (batches - i == 2) {
+                load(x1, g0 + (i + 1) * kN, units);
+                compute(x0, units);
+                compute(x1, units);
+            } else {
+                compute(x0, units);
+            }
         }
-        if (batches - i == 2) {
-            load(x1, g0 + (i + 1) * kU, kBatch);
-            compute(x0, kBatch);
-            compute(x1, kBatch);
-        } else {
-            compute(x0, kBatch);
+        for (int g = g0 + batches * kN; g < g1; ++g) {
+            load(x0, g, McNarrowUnits<1>{});
+            compute(x0, McNarrowUnits<1>{});
         }
-    }
-    for (int g = g0 + batches * kU; g < g1; ++g) {
-        load(x0, g, McNarrowUnits<1>{});
-        compute(x0, McNarrowUnits<1>{});
+    };
+    if (kU > 1 && per >= 32) {
+        pipeline(McNarrowUnits<kU>{});
+    } else {
+        pipeline(McNarrowUnits<1>{});
     }
 
     // Lane l holds rows 16 r + 4s + v of column chunk cl.

@@ -21,10 +21,13 @@ GUARD = 4096
 # tile, N not a multiple of 64 (and not of 8), K not a multiple of the
 # split, a split count above what the plan would take, the bench shapes.
 # The short-K tile shapes too: 256x2048x512 and 300x96x260 on 16x32 tiles,
-# 512^3 and 200x512x640 (ragged M) on 16x64 tiles, unsplit.
+# 512^3 and 200x512x640 (ragged M) on 16x64 tiles, unsplit. Waves with 32
+# groups of K or more load two groups per batch (256x2048x512 on 16x32
+# tiles, 256x256x16384 in 8 ranges), and 64x2064x260 gives them 33 (an odd
+# count: a last group on its own).
 SHAPES = [(1, 16, 4, 1), (5, 96, 260, 3), (16, 4096, 4096, 8), (33, 1040, 1000, 4), (300, 96, 260, 2),
           (256, 512, 2048, 8), (256, 2048, 512, 32), (512, 512, 512, 8), (16, 64, 68, 64), (256, 16384, 256, 64),
-          (200, 512, 640, 4)]
+          (200, 512, 640, 4), (64, 2064, 260, 1)]
 
 
 def run(mc, ring, a, b, m, k, n, splits):

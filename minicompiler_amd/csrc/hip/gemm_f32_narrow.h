@@ -183,13 +183,16 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     // unconditionally where it is issued (the last batch is peeled off): a
     // load under a condition would make the compiler wait for all loads
     // before the next MFMA. A batch is kU groups when each wave has 32 groups
-    // or more, else one group: a short piece gains more from MFMAs that start
-    // after one group's loads than from more loads in flight. Measured on an
-    // MI355X (batches of 1 / 2 / 4 groups): 256x2048x512 on 32x64 tiles 7.8 /
-    // 9.0 / 10.5 us, 512^3 on 16x64 tiles 5.0 / 5.2 / 6.1 us, 16x4096x4096
-    // streamed in 4 K ranges 13.4 / 13.9 / 14.4 us; 256x256x16384 on 32x64
-    // tiles in 8 ranges (32 groups per wave) 21.7 / 21.0 / 24.9 us. The
-    // batching does not change the order of the adds.
+    // or more and the block has one of several K ranges or 16-row tiles,
+    // else one group: a short piece gains more from MFMAs that start after
+    // one group's loads than from more loads in flight. Measured on an MI355X
+    // (batches of 1 / 2 / 4 groups): 256x2048x512 on 32x64 tiles 7.8 / 9.0 /
+    // 10.5 us, 512^3 on 16x64 tiles 5.0 / 5.2 / 6.1 us, 16x4096x4096 streamed
+    // in 4 K ranges 13.4 / 13.9 / 14.4 us; with 32 groups per wave:
+    // 256x256x16384 on 32x64 tiles in 8 ranges 21.7 / 21.0 / 24.9 us,
+    // 256x512x2048 on 16x32 tiles 10.2 / 9.8 / 10.1 us, but 1024x512x2048 on
+    // 32x64 tiles unsplit 18.5 / 20.2 us. The batching does not change the
+    // order of the adds.
     McNarrowRegs<Cfg> x0, x1;
     auto pipeline = [&](auto units) {
         constexpr int kN = decltype(units)::value;
@@ -216,7 +219,7 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
             compute(x0, McNarrowUnits<1>{});
         }
     };
-    if (kU > 1 && per >= 32) {
+    if (kU > 1 && per >= 32 && (depth > 1 || kRG == 1)) {
         pipeline(McNarrowUnits<kU>{});
     } else {
         pipeline(McNarrowUnits<1>{});

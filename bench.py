@@ -21,7 +21,9 @@ graph of back-to-back launches over rotating operand sets (no host launch
 cost; the reference times its GEMMs from a graph, bench_cuda.cpp:445-493).
 Every configuration rotates over buffer sets whose footprint exceeds twice
 the 256 MB MALL, so no timed launch reads operands the last one left on
-chip.
+chip. The other configurations time at least MIN_TIMED_MS of GPU work per
+timed loop (more steps than K when K would run less; `timed_steps` and
+`timed_launches` give the counts); the headline times exactly K steps.
 
 Prints ONE JSON line. `value` is the step's GEMM throughput (TFLOP/s = the
 two GEMMs' 2MNK FLOPs per step / ms_per_step). `roofline` is for the
@@ -40,6 +42,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -60,6 +63,12 @@ MALL_BYTES = 256 << 20
 # Warm-up time of every configuration other than the headline step (which
 # runs exactly --warmup untimed steps).
 WARM_SECONDS = 0.3
+# Every timed loop of the other configs (not the headline, which times
+# exactly --steps steps) runs at least this much GPU work: loops of about a
+# millisecond read slow on an MI355X, whose clock does not hold through short
+# bursts (MLP B=256: 20.9 us per step over 50 steps, 18.4-18.6 over 400 or
+# 2000, same process).
+MIN_TIMED_MS = 20.0
 # Per-launch and per-GEMM timings are the median of this many runs (their range
 # is reported beside them); the headline step time is one run of K steps.
 RUNS = 3
@@ -157,8 +166,16 @@ def rotation_sets(set_bytes: int) -> int:
     return max(1, -(-2 * MALL_BYTES // max(1, set_bytes)) + 1) if set_bytes <= 2 * MALL_BYTES else 1
 
 
+def steps_for(ms_per_step: float, steps: int, min_ms: float) -> int:
+    """`steps`, or more when they would run less than min_ms of GPU work."""
+    if min_ms <= 0:
+        return steps
+    return max(steps, int(math.ceil(min_ms / max(ms_per_step, 1e-4))))
+
+
 def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None,
-               warm_seconds: float = 0.0, sampler: ClockSampler | None = None, launches_first: bool = False) -> dict:
+               warm_seconds: float = 0.0, sampler: ClockSampler | None = None, launches_first: bool = False,
+               min_ms: float = MIN_TIMED_MS) -> dict:
     """W warmup steps (then more until `warm_seconds` have passed), then K
     steps timed between one pair of HIP events on the executable's stream
     (ms_per_step); the K steps are one mc_enqueue_steps call, whose host time
@@ -174,10 +191,25 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     them, so the timed steps run at the clock the GPU holds under this work
     whatever W is (an MI355X takes 30-40 ms of back-to-back work to reach
     it from idle, and idles while the graph is compiled and its buffers are
-    uploaded)."""
+    uploaded).
+
+    min_ms: when K steps (or `reps` launches) would run less GPU work than
+    this, more are timed (steps_for, from a timing of the warm-up steps);
+    `timed_steps` reports the count. 0 times exactly K steps."""
     stream = compiled.stream
     start, stop = mc.Event(), mc.Event()
-    reps = reps or max(steps, 10)
+    given_reps = reps
+
+    def size_loops():
+        nonlocal steps, reps
+        if min_ms > 0:
+            n = max(warmup, 10)
+            start.record(stream)
+            compiled.enqueue_steps(n, sets=rotations)
+            stop.record(stream)
+            compiled.synchronize()
+            steps = steps_for(start.elapsed_ms(stop) / n, steps, min_ms)
+        reps = given_reps or max(steps, 10)
 
     def extra():
         compiled.enqueue_steps(max(warmup, 10), sets=rotations)
@@ -200,11 +232,13 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
 
     if launches_first:
         warm_up_for(warm_seconds, extra)
+        size_loops()
         launch_ms, launch_range = per_launch()
     compiled.enqueue_steps(warmup, sets=rotations)
     compiled.synchronize()
     if not launches_first:
         warm_up_for(warm_seconds, extra)
+        size_loops()
     if sampler is not None:
         sampler.__enter__()
     t0 = time.perf_counter()
@@ -218,8 +252,9 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     total_ms = start.elapsed_ms(stop)
     if not launches_first:
         launch_ms, launch_range = per_launch()
-    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "wall_s": wall, "host_us_per_step": host_us,
-            "launch_ms": launch_ms, "launch_ms_range": launch_range, "launch_reps": reps, "launch_runs": RUNS,
+    return {"total_ms": total_ms, "ms_per_step": total_ms / steps, "timed_steps": steps, "wall_s": wall,
+            "host_us_per_step": host_us, "launch_ms": launch_ms, "launch_ms_range": launch_range, "launch_reps": reps,
+            "launch_runs": RUNS,
             "order": "per-launch timings, then warmup and timed steps" if launches_first else
                      "warmup and timed steps, then per-launch timings"}
 
@@ -240,14 +275,15 @@ def graph_rotation(mc, compiled, make_inputs) -> tuple[list, list]:
 
 
 def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0,
-              sampler: ClockSampler | None = None, launches_first: bool = False) -> dict:
+              sampler: ClockSampler | None = None, launches_first: bool = False,
+              min_ms: float = MIN_TIMED_MS) -> dict:
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
     # Graph replay captures once per binding: no rotation for it.
     rot, bufs = (None, None) if options and options.get("graph") else graph_rotation(mc, c, lambda: [x])
     t = time_graph(mc, c, steps, warmup, rot, warm_seconds=warm_seconds, sampler=sampler,
-                   launches_first=launches_first)
+                   launches_first=launches_first, min_ms=min_ms)
     work = node_work(c.graph(), c.launch_nodes)
     names = c.launch_names
     kernels = [rate_entry(n, w, ms) for n, w, ms in zip(names, work, t["launch_ms"])]
@@ -270,17 +306,20 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
     k["ms_range"] = t["launch_ms_range"][0]
     k["gbs_range"] = [k["bytes"] / (ms * 1e-3) / 1e9 for ms in reversed(k["ms_range"])]
     return {"config": name, "dims": dims, "buffer_sets": len(rot), "kernel": k, "ms_per_step": t["ms_per_step"],
+            "timed_steps": t["timed_steps"], "launch_reps": t["launch_reps"],
             "host_us_per_step": t["host_us_per_step"], "gbs": k["gbs"], "frac": k["frac"]}
 
 
-def time_gemm(mc, launches, steps: int, warmup: int) -> dict:
+def time_gemm(mc, launches, steps: int, warmup: int, min_ms: float = MIN_TIMED_MS) -> dict:
     """Mean duration of one launch, over `steps` back-to-back launches that
     cycle through `launches` (one closure per operand set, each enqueueing
     on the stream it is given), after `warmup` rounds and WARM_SECONDS of
-    warm-up. Timed two ways, RUNS runs each (median and range): `graph`, a
-    HIP graph of the `steps` launches captured once and replayed between one
-    pair of HIP events (no host launch cost, the reference's GEMM timing);
-    `direct`, the same launches issued one by one from the host."""
+    warm-up; more launches when `steps` would run less than min_ms of GPU
+    work (`timed_steps` reports the count). Timed two ways, RUNS runs each
+    (median and range): `graph`, a HIP graph of the launches captured once
+    and replayed between one pair of HIP events (no host launch cost, the
+    reference's GEMM timing); `direct`, the same launches issued one by one
+    from the host."""
     s = mc.Stream()
     for _ in range(warmup):
         for f in launches:
@@ -295,9 +334,15 @@ def time_gemm(mc, launches, steps: int, warmup: int) -> dict:
         s.synchronize()
 
     warm_up_for(WARM_SECONDS, extra)
-    g = mc.CapturedGraph(s, issue)
     start, stop = mc.Event(), mc.Event()
-    out = {}
+    if min_ms > 0:
+        start.record(s)
+        issue(s)
+        stop.record(s)
+        s.synchronize()
+        steps = steps_for(start.elapsed_ms(stop) / steps, steps, min_ms)
+    g = mc.CapturedGraph(s, issue)
+    out = {"timed_steps": steps}
     for mode in ("graph", "direct"):
         runs = []
         for _ in range(RUNS):
@@ -333,7 +378,8 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
         ms = t["graph"]["ms"]
         flop = 2.0 * m * n * k
         e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "operand_sets": len(sets), "ms": ms,
-             "ms_range": t["graph"]["ms_range"], "timing": "hip graph of back-to-back launches",
+             "ms_range": t["graph"]["ms_range"], "timed_launches": t["timed_steps"],
+             "timing": "hip graph of back-to-back launches",
              "ms_direct_launches": t["direct"]["ms"], "tflops": flop / (ms * 1e-3) / 1e12}
         e["frac"] = e["tflops"] / PEAK_FP32_TFLOPS
         if m <= 32:  # HBM-bound skinny shape: report bytes too
@@ -398,7 +444,8 @@ def bench_gemm_lowp(mc, shapes, steps: int, warmup: int) -> list[dict]:
             tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
             out.append({"m": m, "n": n, "k": k, "kernel": kernel, "inputs": "bf16" if dtype == 1 else "fp16",
                         "operand_sets": len(sets), "ms": ms, "ms_range": t["graph"]["ms_range"],
-                        "ms_direct_launches": t["direct"]["ms"], "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
+                        "timed_launches": t["timed_steps"], "ms_direct_launches": t["direct"]["ms"], "tflops": tf,
+                        "frac": tf / PEAK_BF16_TFLOPS})
             log(f"gemm {kernel} {m}x{n}x{k}: {ms:.3f} ms {tf:.1f} TFLOP/s ({len(sets)} operand sets)")
             del sets, launches
     return out
@@ -640,6 +687,7 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
             for mode, opts in (("direct", None), ("graph_replay", {"graph": 1}), ("autotuned", {"autotune": 1})):
                 r = bench_mlp(mc, b, max(args.steps, 50), args.warmup, opts, WARM_SECONDS)
                 entry[mode] = {"ms_per_step": r["timing"]["ms_per_step"], "tflops": r["value"],
+                               "timed_steps": r["timing"]["timed_steps"],
                                "launches": r["compiled"].kernel_launches, "buffer_sets": r["buffer_sets"],
                                "host_us_per_step": r["timing"]["host_us_per_step"],
                                "launch_ms": r["timing"]["launch_ms"]}
@@ -713,7 +761,7 @@ def main() -> int:
 
     if args.workload == "mlp":
         r = bench_mlp(mc, args.batch, args.steps, args.warmup, sampler=sampler, warm_seconds=WARM_SECONDS,
-                      launches_first=True)
+                      launches_first=True, min_ms=0.0)  # exactly --steps timed steps
         ks = r["kernels"]
         dom = max(ks, key=lambda e: e["ms"])
         line.update({"value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["timing"]["ms_per_step"],
@@ -735,13 +783,14 @@ def main() -> int:
         k = bench_elementwise_graph(mc, "copy_neg", {"M": 8192, "N": 4096}, lambda n: mc.uniform(n, 1, -1.0, 1.0),
                                     args.steps, args.warmup)
         line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",
+                     "steps": k["timed_steps"],
                      "config": {"workload": "copy_neg (counter calibration)", **k["dims"]},
                      "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
     elif args.workload in ("gelu", "batchnorm"):
         k = next(iter(cfgs.values()))
         line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",
-                     "config": {"workload": k["config"], **k["dims"]},
+                     "steps": k["timed_steps"], "config": {"workload": k["config"], **k["dims"]},
                      "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
         if "cpu_baseline" in k:

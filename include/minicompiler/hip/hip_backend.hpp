@@ -113,7 +113,9 @@ struct HipOptions {
     bool split_fold = false;
     // The FP32 ring tile configuration of double_buffered / split_k matmuls
     // without autotune (MCHIP_RING_*: 0 the planner's own, 1 wide 128x128,
-    // 2 mid 64x128, 3 big 256x256, 4 thin 32x128). Same bits as the planner's.
+    // 2 mid 64x128, 3 big 256x256, 4 thin 32x128, 5 narrow tiles for split_k,
+    // 6 wide8: 128x128 in one 8-wave block per CU). The ring configurations
+    // give the same bits as each other.
     int ring_config = 0;
 };
 

@@ -73,7 +73,7 @@ MC_API void mc_release(void* handle); /* capi.cpp:233-235 */
 
 /* mc_compile from graph text, with backend options
  * "matmul=NAME,vectorize=0|1,device=N,epilogue=0|1,tc_convert=0|1,graph=0|1,
- * autotune=0|1,ring=auto|wide|mid|big|thin" (graph=1: mc_enqueue captures its
+ * autotune=0|1,split_fold=0|1,ring=auto|wide|wide8|mid|big|thin|narrow" (graph=1: mc_enqueue captures its
  * launches into a HIP graph once and replays it; rebinding buffers captures
  * again. autotune=1: an auto FP32 matmul's K split and tile configuration
  * are chosen by timing the candidates on the device at compile time, kept
@@ -161,7 +161,7 @@ MC_API int mc_generate_elementwise_kernel(const char* program, const char* input
  * `acc_input` is the accumulated value; the others are read by access class
  * against `out_shape`), as the executable generates it for a matmul with a
  * fused elementwise consumer, on GEMM body `body`: "two_stage" (or NULL),
- * "ring_big", "ring_wide", "ring_mid", "ring_thin", "narrow16",
+ * "ring_big", "ring_wide", "ring_wide8", "ring_mid", "ring_thin", "narrow16",
  * "narrow32", "narrow16x64", "narrow16x32", "bf16", "f16". Works without a
  * device. */
 MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
@@ -183,7 +183,9 @@ MC_API int mc_launch_matmul(int kernel, const float* a, const float* b, float* c
  * configuration forced (no counterpart in the reference, whose tiles are
  * fixed; the autotuner picks one, see the `autotune` option): ring_cfg 0 =
  * the planner's own, 1 = wide (128x128 tiles), 2 = mid (64x128), 3 = big
- * (256x256), 4 = thin (32x128). The configuration does not change the bits.
+ * (256x256), 4 = thin (32x128), 5 = narrow (32x64 or 16x64 narrow tiles,
+ * split_k only, their own accumulation order), 6 = wide8 (128x128 tiles in
+ * one 8-wave block per CU). The ring configurations give the same bits.
  * hipErrorInvalidValue when it cannot run the product (K not a multiple of
  * 32, N not of 4, operands not 16-byte aligned) or for other kernels. */
 MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k,

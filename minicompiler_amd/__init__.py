@@ -590,7 +590,7 @@ def noalloc_scratch_bytes() -> int:
     return int(library().mc_noalloc_scratch_bytes())
 
 
-RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4, "narrow": 5}
+RING_CONFIGS = {"auto": 0, "wide": 1, "mid": 2, "big": 3, "thin": 4, "narrow": 5, "wide8": 6}
 
 
 def launch_matmul_cfg(kernel: int | str, a: int, b: int, c: int, m: int, n: int, k: int, stream=None,

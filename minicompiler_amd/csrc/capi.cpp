@@ -130,12 +130,14 @@ Result<hip::HipOptions> parse_options(const char* spec) {
         } else if (key == "split_fold") {
             o.split_fold = value != "0" && value != "false";
         } else if (key == "ring") {
-            static const char* const names[] = {"auto", "wide", "mid", "big", "thin", "narrow"};
+            static const char* const names[] = {"auto", "wide", "mid", "big", "thin", "narrow", "wide8"};
             int cfg = -1;
-            for (int i = 0; i < 6; ++i) {
+            for (int i = 0; i < 7; ++i) {
                 if (value == names[i]) cfg = i;
             }
-            if (cfg < 0) return Error{"option ring=" + value + ": expected auto, wide, mid, big, thin or narrow"};
+            if (cfg < 0) {
+                return Error{"option ring=" + value + ": expected auto, wide, wide8, mid, big, thin or narrow"};
+            }
             o.ring_config = cfg;
         } else if (key == "ew_nt_loads") {
             o.nontemporal_loads = value != "0" && value != "false";
@@ -746,6 +748,7 @@ MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, 
         {"two_stage", hip::GemmBody::F32Mfma, &hip::kGemmF32MfmaSource},
         {"ring_big", hip::GemmBody::F32RingBig, &hip::kGemmF32RingSource},
         {"ring_wide", hip::GemmBody::F32RingWide, &hip::kGemmF32RingSource},
+        {"ring_wide8", hip::GemmBody::F32RingWide8, &hip::kGemmF32RingSource},
         {"ring_mid", hip::GemmBody::F32RingMid, &hip::kGemmF32RingSource},
         {"ring_thin", hip::GemmBody::F32RingThin, &hip::kGemmF32RingSource},
         {"narrow16", hip::GemmBody::F32Narrow16, &hip::kGemmF32NarrowSource},

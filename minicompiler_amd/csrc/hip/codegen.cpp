@@ -303,6 +303,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         return {os.str()};
     }
     const char* bounds = body == GemmBody::F32RingBig || body == GemmBody::F32RingThin ? "256, 1"
+                         : body == GemmBody::F32RingWide8                              ? "512, 1"
                          : is_narrow_body(body)                                        ? "256"
                                                                                        : "256, 2";
     os << "extern \"C\" __global__ void __launch_bounds__(" << bounds << ")\n" << kGemmEpilogueKernelName
@@ -320,6 +321,7 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
         const char* cfg = body == GemmBody::F32RingBig    ? "McRingBig"
                           : body == GemmBody::F32RingThin ? "McRingThin"
                           : body == GemmBody::F32RingMid  ? "McRingMid"
+                          : body == GemmBody::F32RingWide8 ? "McRingWide8"
                                                           : "McRingWide";
         os << "\tmc_gemm_f32_ring<" << cfg << ">(a, b, c, "
            << mnk << ", " << split << ", partial, counters, epi);\n}\n\n";

@@ -81,6 +81,7 @@ enum class GemmBody {
     F32Mfma,      // fp32 operands, FP32 matrix cores, 128x128 tiles, 256 lanes, split K (gemm_f32_mfma.h)
     F32RingBig,   // the same arithmetic, LDS ring, persistent (gemm_f32_ring.h): 256x256 tiles, one block per CU
     F32RingWide,  // likewise, 128x128 tiles, 2 stages, up to two blocks per CU
+    F32RingWide8,  // likewise, 128x128 tiles, one block of 8 waves per CU
     F32RingThin,  // likewise, 32x128 tiles (M <= 32, or when the autotuner picks it), 6 stages
     F32RingMid,   // likewise, 64x128 tiles, 3 stages, up to two blocks per CU (autotuner only)
     F32Narrow16,  // fp32 operands, 16x64 tiles on 16x16x4 MFMAs, K split over waves (gemm_f32_narrow.h), M <= 16
@@ -98,6 +99,7 @@ inline bool is_narrow_body(GemmBody body) {
 
 inline bool is_f32_body(GemmBody body) {
     return body == GemmBody::F32Mfma || body == GemmBody::F32RingBig || body == GemmBody::F32RingWide ||
+           body == GemmBody::F32RingWide8 ||
            body == GemmBody::F32RingThin || body == GemmBody::F32RingMid || is_narrow_body(body);
 }
 

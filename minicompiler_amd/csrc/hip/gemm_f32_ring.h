@@ -88,6 +88,11 @@ struct McRingCfg {
 //         than a 4-stage direct-fetch form with one block per CU, on every
 //         shape it is chosen for; with one block of 4 waves per SIMD set a
 //         direct fetch instruction holds up the wave's MFMA issue);
+//   wide8: the same tiles in one block of 8 waves (two per SIMD, 32x64 per
+//         wave), for grids of at most one 128x128 tile per CU: a wave's
+//         waits overlap the other wave's MFMAs (8192x512x2048 131.1 against
+//         134.0 us, 2048^3 130.9 against 134.1 us on an MI355X; 256x256
+//         tiles with 8 waves gained nothing);
 //   thin: for M <= 32 (HBM-bound on B): 32x128 tiles, 4 waves of 32x32, 6
 //         stages of 20 KiB keeping more of B in flight, so a 128-row tile's
 //         MFMA work on clamped rows no longer dominates;
@@ -97,6 +102,7 @@ struct McRingCfg {
 //         unsplit on mid: 23.8 us against 31.4 us for wide with 2 splits).
 using McRingBig = McRingCfg<256, 256, 128, 128, 4, 2>;
 using McRingWide = McRingCfg<128, 128, 64, 64, 4, 2, true>;
+using McRingWide8 = McRingCfg<128, 128, 32, 64, 8, 2, true>;
 using McRingThin = McRingCfg<32, 128, 32, 32, 4, 6>;
 using McRingMid = McRingCfg<64, 128, 32, 64, 4, 3>;
 

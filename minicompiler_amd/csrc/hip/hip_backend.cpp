@@ -580,6 +580,13 @@ private:
             case MCHIP_RING_BIG: return GemmBody::F32RingBig;
             case MCHIP_RING_THIN: return GemmBody::F32RingThin;
             case MCHIP_RING_WIDE: return GemmBody::F32RingWide;
+            case MCHIP_RING_WIDE8:
+                if (l.ring_cfg == MCHIP_RING_WIDE8) return GemmBody::F32RingWide8;
+                // The planner's 8-wave choice, with a group in the store: the
+                // 4-wave blocks are faster there (the MLP's GEMM2 with b2 +
+                // residual, 140.9 against 142.9 us on an MI355X).
+                l.ring_cfg = MCHIP_RING_WIDE;
+                return GemmBody::F32RingWide;
             case MCHIP_RING_MID: return GemmBody::F32RingMid;
             default: return GemmBody::F32Mfma;
         }

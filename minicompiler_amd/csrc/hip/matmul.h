@@ -50,7 +50,10 @@ int mchip_matmul_blocks_per_cu(int kernel);
  *   MCHIP_RING_BIG   one persistent block of 4 waves per CU, 256x256 tiles;
  *   MCHIP_RING_WIDE  up to two persistent blocks of 4 waves per CU, 128x128
  *                    tiles, the fetch staged through registers;
- *   MCHIP_RING_THIN  for m <= 32: 32x128 tiles, 6 LDS stages.
+ *   MCHIP_RING_THIN  for m <= 32: 32x128 tiles, 6 LDS stages;
+ *   MCHIP_RING_WIDE8 128x128 tiles in one block of 8 waves per CU, in place
+ *                    of wide when an unsplit product has at most one tile
+ *                    per CU.
  * The choice minimises (rounds of tiles per CU) x (work per tile) / (the
  * configuration's measured efficiency). *grid receives the number of
  * blocks, *block the lanes per block.
@@ -64,7 +67,8 @@ enum {
     MCHIP_RING_MID = 2,
     MCHIP_RING_BIG = 3,
     MCHIP_RING_THIN = 4,
-    MCHIP_RING_NARROW = 5
+    MCHIP_RING_NARROW = 5,
+    MCHIP_RING_WIDE8 = 6
 };
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);

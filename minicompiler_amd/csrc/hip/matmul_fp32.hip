@@ -159,6 +159,7 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma_f32(const float* __restric
 
 using RingBig = McRingBig;
 using RingWide = McRingWide;
+using RingWide8 = McRingWide8;
 using RingThin = McRingThin;
 using RingMid = McRingMid;
 constexpr int kRBKRing = RingWide::kBK;
@@ -352,6 +353,9 @@ int launch_mfma_f32(bool double_buffer, const float* a, const float* b, float* c
     } else if (ring == MCHIP_RING_BIG) {
         hipLaunchKernelGGL((matmul_ring_f32<RingBig, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws, ctr);
+    } else if (ring == MCHIP_RING_WIDE8) {
+        hipLaunchKernelGGL((matmul_ring_f32<RingWide8, 1>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
+                           k, k_split, depth, out_ws, ctr);
     } else if (ring == MCHIP_RING_WIDE) {
         hipLaunchKernelGGL((matmul_ring_f32<RingWide, 2>), dim3(ring_grid), dim3(ring_block), 0, stream, a, b, c, m, n,
                            k, k_split, depth, out_ws, ctr);
@@ -387,7 +391,7 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
     }
     if (cfg != MCHIP_RING_NONE) {
         // A forced configuration: its tiles, in persistent blocks (at most
-        // one per CU for big and thin, two for wide and mid).
+        // one per CU for big, thin and wide8, two for wide and mid).
         long long bm = 0, bn = 0, per_cu = 1;
         unsigned threads = 0;
         switch (cfg) {
@@ -395,6 +399,7 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
             case MCHIP_RING_WIDE: bm = RingWide::kBM, bn = RingWide::kBN, threads = RingWide::kThreads, per_cu = 2; break;
             case MCHIP_RING_MID: bm = RingMid::kBM, bn = RingMid::kBN, threads = RingMid::kThreads, per_cu = 2; break;
             case MCHIP_RING_THIN: bm = RingThin::kBM, bn = RingThin::kBN, threads = RingThin::kThreads; break;
+            case MCHIP_RING_WIDE8: bm = RingWide8::kBM, bn = RingWide8::kBN, threads = RingWide8::kThreads; break;
             default: return MCHIP_RING_NONE;
         }
         const long long units = ((m + bm - 1) / bm) * ((n + bn - 1) / bn) * depth;
@@ -425,6 +430,11 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
         return MCHIP_RING_BIG;
     }
     *grid = static_cast<unsigned>(wide_grid);
+    if (depth == 1 && t128 <= cus) {
+        // One tile per CU at most: the 8-wave block (two waves per SIMD).
+        *block = RingWide8::kThreads;
+        return MCHIP_RING_WIDE8;
+    }
     *block = RingWide::kThreads;
     return MCHIP_RING_WIDE;
 }

@@ -153,6 +153,7 @@ def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, ou
 
 @pytest.mark.parametrize("body,call", [("ring_big", "mc_gemm_f32_ring<McRingBig>"),
                                        ("ring_wide", "mc_gemm_f32_ring<McRingWide>"),
+                                       ("ring_wide8", "mc_gemm_f32_ring<McRingWide8>"),
                                        ("ring_thin", "mc_gemm_f32_ring<McRingThin>"),
                                        ("ring_mid", "mc_gemm_f32_ring<McRingMid>"),
                                        ("narrow16", "mc_gemm_f32_narrow<McNarrow16>"),

@@ -60,8 +60,9 @@ def test_fused_epilogue_on_the_ring_equals_the_two_stage_body(device, mc, oracle
     # The MLP block: GEMM1 (B x 2048 x 512) runs the ring (two 128x128 blocks
     # per CU at B=4096, 256x256 tiles at B=8192) with bias+GELU fused into
     # its store; GEMM2 (B x 512 x 2048) the 128x128 ring with one block per
-    # CU, with b2 + residual. The vectorized graph runs the two-stage body
-    # (also fused): identical bits throughout.
+    # CU, with b2 + residual (a fused GEMM keeps the 4-wave blocks where an
+    # unfused one would take the 8-wave block). The vectorized graph runs the
+    # two-stage body (also fused): identical bits throughout.
     dims = {"B": batch}
     ring = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"matmul": "double_buffered"})
     two = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"matmul": "vectorized"})
@@ -106,7 +107,7 @@ def test_forced_ring_configurations_give_the_plans_bits(device, mc, oracle, m, k
     ws_bytes = mc.matmul_workspace_bytes(kernel, m, n, splits) if splits > 1 else 0
     ws = mc.DeviceBuffer(ws_bytes) if ws_bytes else None
     ref = run_cfg(mc, kernel, "wide", da, db, m, n, k, splits, ws)
-    for ring in ("mid", "big", "thin"):
+    for ring in ("mid", "big", "thin", "wide8"):
         got = run_cfg(mc, kernel, ring, da, db, m, n, k, splits, ws)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), ring
     exact, absdot = oracle.gemm_f64(a, b, m, k, n)
@@ -146,6 +147,28 @@ def test_a_forced_configuration_the_product_cannot_take_is_an_error(device, mc):
     da, db, dc = mc.DeviceBuffer(4 * 64 * 40), mc.DeviceBuffer(4 * 40 * 64), mc.DeviceBuffer(4 * 64 * 64)
     with pytest.raises(mc.HipError):
         mc.launch_matmul_cfg("double_buffered", da.ptr, db.ptr, dc.ptr, 64, 64, 40, None, 1, None, "mid")
+
+
+def test_an_unfused_product_with_a_tile_per_cu_takes_the_8_wave_block_with_the_same_bits(device, mc, oracle):
+    # 2048^3 double_buffered: 256 tiles of 128x128 on 256 CUs run as one
+    # 8-wave block each (wide8); forced wide (4-wave blocks) and the
+    # two-stage body give the same bits, and a fused graph of the same
+    # product with ring=wide8 compiles the 8-wave body.
+    m = n = k = 2048
+    if int(device["cu_count"]) != 256:
+        pytest.skip("tile counts are for 256 CUs")
+    a = oracle.uniform(m * k, 25, -1.0, 1.0)
+    b = oracle.uniform(k * n, 26, -1.0, 1.0)
+    da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
+    planned = run_cfg(mc, "double_buffered", "auto", da, db, m, n, k, 1, None)
+    for ring in ("wide8", "wide"):
+        got = run_cfg(mc, "double_buffered", ring, da, db, m, n, k, 1, None)
+        assert np.array_equal(got.view(np.uint32), planned.view(np.uint32)), ring
+    two = run(mc, "vectorized", da, db, m, n, k)
+    assert np.array_equal(two.view(np.uint32), planned.view(np.uint32))
+    g = mc.Compiled(path=mc.graph_path("matmul_bias_relu"), dims={"M": m, "K": k, "N": n},
+                    options={"matmul": "double_buffered", "ring": "wide8"})
+    assert "mc_gemm_f32_ring<McRingWide8>" in "\n".join(g.kernel_sources), g.launch_names
 
 
 def test_the_ring_option_gives_one_set_of_bits_for_every_ring_configuration(device, mc, oracle):

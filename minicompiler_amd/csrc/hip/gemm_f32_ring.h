@@ -89,10 +89,11 @@ struct McRingCfg {
 //         shape it is chosen for; with one block of 4 waves per SIMD set a
 //         direct fetch instruction holds up the wave's MFMA issue);
 //   wide8: the same tiles in one block of 8 waves (two per SIMD, 32x64 per
-//         wave), for grids of at most one 128x128 tile per CU: a wave's
-//         waits overlap the other wave's MFMAs (8192x512x2048 131.1 against
-//         134.0 us, 2048^3 130.9 against 134.1 us on an MI355X; 256x256
-//         tiles with 8 waves gained nothing);
+//         wave), for grids of at most one 128x128 tile (or tile-split) per
+//         CU: a wave's waits overlap the other wave's MFMAs (8192x512x2048
+//         131.1 against 134.0 us, 2048^3 130.9 against 134.1 us, 1024^3 in 4
+//         splits 27.2 against 27.7 us on an MI355X; 256x256 tiles with 8
+//         waves gained nothing);
 //   thin: for M <= 32 (HBM-bound on B): 32x128 tiles, 4 waves of 32x32, 6
 //         stages of 20 KiB keeping more of B in flight, so a 128-row tile's
 //         MFMA work on clamped rows no longer dominates;

@@ -52,8 +52,8 @@ int mchip_matmul_blocks_per_cu(int kernel);
  *                    tiles, the fetch staged through registers;
  *   MCHIP_RING_THIN  for m <= 32: 32x128 tiles, 6 LDS stages;
  *   MCHIP_RING_WIDE8 128x128 tiles in one block of 8 waves per CU, in place
- *                    of wide when an unsplit product has at most one tile
- *                    per CU.
+ *                    of wide when the product has at most one tile (or
+ *                    tile-split) per CU.
  * The choice minimises (rounds of tiles per CU) x (work per tile) / (the
  * configuration's measured efficiency). *grid receives the number of
  * blocks, *block the lanes per block.

@@ -430,8 +430,9 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
         return MCHIP_RING_BIG;
     }
     *grid = static_cast<unsigned>(wide_grid);
-    if (depth == 1 && t128 <= cus) {
-        // One tile per CU at most: the 8-wave block (two waves per SIMD).
+    if (t128 <= cus) {
+        // One tile (or tile-split) per CU at most: the 8-wave block (two
+        // waves per SIMD; 1024^3 in 4 splits 27.2 against 27.7 us).
         *block = RingWide8::kThreads;
         return MCHIP_RING_WIDE8;
     }

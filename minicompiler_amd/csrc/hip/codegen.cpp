@@ -329,7 +329,8 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
     // Split K: the partial sums added in split order (a left fold from split
     // 0's value), then the epilogue. A lane issues `chunk` split loads before
     // it adds any (indices past the last split clamped to it, their adds
-    // skipped), so they are in flight together.
+    // skipped), so they are in flight together; the loads are non-temporal
+    // (each partial is read once; see sum_splits_chunked).
     const int chunk = constant ? std::max(1, std::min(fixed.depth - 1, 64)) : 16;
     os << "extern \"C\" __global__ void __launch_bounds__(256)\n" << kSumSplitsEpilogueKernelName
        << "(const float* __restrict__ partial, float* __restrict__ c, unsigned count, int splits_arg, "
@@ -337,13 +338,13 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
        << (constant ? "\t(void)splits_arg;\n\tconst int splits = " + std::to_string(fixed.depth) + ";\n"
                     : std::string("\tconst int splits = splits_arg;\n"))
        << "\tfor (unsigned i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {\n"
-       << "\t\tfloat s = partial[i];\n"
+       << "\t\tfloat s = __builtin_nontemporal_load(partial + i);\n"
        << "\t\tfor (int z0 = 1; z0 < splits; z0 += " << chunk << ") {\n"
        << "\t\t\tfloat p[" << chunk << "];\n"
        << "#pragma unroll\n"
        << "\t\t\tfor (int j = 0; j < " << chunk << "; ++j) {\n"
        << "\t\t\t\tconst int z = z0 + j < splits ? z0 + j : splits - 1;\n"
-       << "\t\t\t\tp[j] = partial[(unsigned long long)z * count + i];\n"
+       << "\t\t\t\tp[j] = __builtin_nontemporal_load(partial + (unsigned long long)z * count + i);\n"
        << "\t\t\t}\n"
        << "#pragma unroll\n"
        << "\t\t\tfor (int j = 0; j < " << chunk << "; ++j)\n"

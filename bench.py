@@ -64,11 +64,17 @@ MALL_BYTES = 256 << 20
 # runs exactly --warmup untimed steps).
 WARM_SECONDS = 0.3
 # Every timed loop of the other configs (not the headline, which times
-# exactly --steps steps) runs at least this much GPU work: loops of about a
-# millisecond read slow on an MI355X, whose clock does not hold through short
-# bursts (MLP B=256: 20.9 us per step over 50 steps, 18.4-18.6 over 400 or
-# 2000, same process).
+# exactly --steps steps) runs at least this much GPU work (--min-timed-ms):
+# loops of about a millisecond read slow on an MI355X, whose clock does not
+# hold through short bursts (MLP B=256: 20.9 us per step over 50 steps,
+# 18.4-18.6 over 400 or 2000, same process). Runs under rocprofv3 pass 0:
+# the many graph replays it adds to the GEMM rows crashed the traced process
+# (a host fault after the 8192^3 row, 3 of 3 runs; none without the tracer,
+# none under it with 0).
 MIN_TIMED_MS = 20.0
+# Launches per captured HIP graph in the GEMM rows (replayed as often as the
+# timed launches need).
+GRAPH_LAUNCHES = 256
 # Per-launch and per-GEMM timings are the median of this many runs (their range
 # is reported beside them); the headline step time is one run of K steps.
 RUNS = 3
@@ -166,8 +172,10 @@ def rotation_sets(set_bytes: int) -> int:
     return max(1, -(-2 * MALL_BYTES // max(1, set_bytes)) + 1) if set_bytes <= 2 * MALL_BYTES else 1
 
 
-def steps_for(ms_per_step: float, steps: int, min_ms: float) -> int:
-    """`steps`, or more when they would run less than min_ms of GPU work."""
+def steps_for(ms_per_step: float, steps: int, min_ms: float | None) -> int:
+    """`steps`, or more when they would run less than min_ms (None:
+    MIN_TIMED_MS) of GPU work."""
+    min_ms = MIN_TIMED_MS if min_ms is None else min_ms
     if min_ms <= 0:
         return steps
     return max(steps, int(math.ceil(min_ms / max(ms_per_step, 1e-4))))
@@ -175,7 +183,7 @@ def steps_for(ms_per_step: float, steps: int, min_ms: float) -> int:
 
 def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int | None = None,
                warm_seconds: float = 0.0, sampler: ClockSampler | None = None, launches_first: bool = False,
-               min_ms: float = MIN_TIMED_MS) -> dict:
+               min_ms: float | None = None) -> dict:
     """W warmup steps (then more until `warm_seconds` have passed), then K
     steps timed between one pair of HIP events on the executable's stream
     (ms_per_step); the K steps are one mc_enqueue_steps call, whose host time
@@ -194,15 +202,16 @@ def time_graph(mc, compiled, steps: int, warmup: int, rotations=None, reps: int 
     uploaded).
 
     min_ms: when K steps (or `reps` launches) would run less GPU work than
-    this, more are timed (steps_for, from a timing of the warm-up steps);
-    `timed_steps` reports the count. 0 times exactly K steps."""
+    this (None: MIN_TIMED_MS), more are timed (steps_for, from a timing of
+    the warm-up steps); `timed_steps` reports the count. 0 times exactly K
+    steps."""
     stream = compiled.stream
     start, stop = mc.Event(), mc.Event()
     given_reps = reps
 
     def size_loops():
         nonlocal steps, reps
-        if min_ms > 0:
+        if (MIN_TIMED_MS if min_ms is None else min_ms) > 0:
             n = max(warmup, 10)
             start.record(stream)
             compiled.enqueue_steps(n, sets=rotations)
@@ -276,7 +285,7 @@ def graph_rotation(mc, compiled, make_inputs) -> tuple[list, list]:
 
 def bench_mlp(mc, batch: int, steps: int, warmup: int, options=None, warm_seconds: float = 0.0,
               sampler: ClockSampler | None = None, launches_first: bool = False,
-              min_ms: float = MIN_TIMED_MS) -> dict:
+              min_ms: float | None = None) -> dict:
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch}, options=options)
     x = mc.uniform(batch * 512, 1, -1.0, 1.0)
     c.upload([x])
@@ -310,7 +319,7 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
             "host_us_per_step": t["host_us_per_step"], "gbs": k["gbs"], "frac": k["frac"]}
 
 
-def time_gemm(mc, launches, steps: int, warmup: int, min_ms: float = MIN_TIMED_MS) -> dict:
+def time_gemm(mc, launches, steps: int, warmup: int, min_ms: float | None = None) -> dict:
     """Mean duration of one launch, over `steps` back-to-back launches that
     cycle through `launches` (one closure per operand set, each enqueueing
     on the stream it is given), after `warmup` rounds and WARM_SECONDS of
@@ -335,22 +344,29 @@ def time_gemm(mc, launches, steps: int, warmup: int, min_ms: float = MIN_TIMED_M
 
     warm_up_for(WARM_SECONDS, extra)
     start, stop = mc.Event(), mc.Event()
-    if min_ms > 0:
+    # The graph holds at most GRAPH_LAUNCHES launches and is replayed as many
+    # times as the timed launches need.
+    replays = 1
+    if (MIN_TIMED_MS if min_ms is None else min_ms) > 0:
         start.record(s)
         issue(s)
         stop.record(s)
         s.synchronize()
-        steps = steps_for(start.elapsed_ms(stop) / steps, steps, min_ms)
+        want = steps_for(start.elapsed_ms(stop) / steps, steps, min_ms)
+        if want > steps:
+            steps = min(want, GRAPH_LAUNCHES)
+            replays = -(-want // steps)
     g = mc.CapturedGraph(s, issue)
-    out = {"timed_steps": steps}
+    out = {"timed_steps": steps * replays}
     for mode in ("graph", "direct"):
         runs = []
         for _ in range(RUNS):
             start.record(s)
-            g.launch() if mode == "graph" else issue(s)
+            for _ in range(replays):
+                g.launch() if mode == "graph" else issue(s)
             stop.record(s)
             s.synchronize()
-            runs.append(start.elapsed_ms(stop) / steps)
+            runs.append(start.elapsed_ms(stop) / (steps * replays))
         out[mode] = {"ms": statistics.median(runs), "ms_range": [min(runs), max(runs)]}
     del g
     return out
@@ -721,6 +737,7 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
 
 
 def main() -> int:
+    global MIN_TIMED_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     # About 70 ms of timed work at B=8192; the 300 warmup steps (about 100 ms)
@@ -734,7 +751,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the headline's CPU baseline")
     ap.add_argument("--config-cpu-seconds", type=float, default=1.5, help="each other config's CPU baseline")
+    ap.add_argument("--min-timed-ms", type=float, default=MIN_TIMED_MS,
+                    help="GPU work per timed loop of the other configs (0 under rocprofv3)")
     args = ap.parse_args()
+    MIN_TIMED_MS = args.min_timed_ms
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the multi-GPU sharding is a design only "

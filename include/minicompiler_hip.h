@@ -162,8 +162,8 @@ MC_API int mc_generate_elementwise_kernel(const char* program, const char* input
  * against `out_shape`), as the executable generates it for a matmul with a
  * fused elementwise consumer, on GEMM body `body`: "two_stage" (or NULL),
  * "ring_big", "ring_wide", "ring_wide8", "ring_mid", "ring_thin", "narrow16",
- * "narrow32", "narrow16x64", "narrow16x32", "bf16", "f16". Works without a
- * device. */
+ * "narrow32", "narrow16x64", "narrow16x32", "narrow64", "bf16", "f16". Works
+ * without a device. */
 MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, const char* input_shapes,
                                             const char* out_shape, int vectorized_operands, const char* body,
                                             char* out, int size);

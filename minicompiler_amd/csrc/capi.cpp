@@ -755,6 +755,7 @@ MC_API int mc_generate_gemm_epilogue_kernel(const char* program, int acc_input, 
         {"narrow32", hip::GemmBody::F32Narrow32, &hip::kGemmF32NarrowSource},
         {"narrow16x64", hip::GemmBody::F32Narrow16x64, &hip::kGemmF32NarrowSource},
         {"narrow16x32", hip::GemmBody::F32Narrow16x32, &hip::kGemmF32NarrowSource},
+        {"narrow64", hip::GemmBody::F32Narrow64, &hip::kGemmF32NarrowSource},
         {"bf16", hip::GemmBody::Bf16Fast, &hip::kGemm16FastSource},
         {"f16", hip::GemmBody::F16Fast, &hip::kGemm16FastSource},
     };

@@ -88,13 +88,14 @@ enum class GemmBody {
     F32Narrow32,  // likewise, 32x64 tiles (split_k products with at most one tile per CU)
     F32Narrow16x64,  // likewise, 16x64 tiles for M > 16 (short K, more tiles than 32x64 give)
     F32Narrow16x32,  // likewise, 16x32 tiles
+    F32Narrow64,  // likewise, 64x64 tiles
     Bf16Fast,     // bf16 operands in HBM, 256x256 tiles, 512 lanes, one block per tile
     F16Fast,      // fp16 operands, likewise
 };
 
 inline bool is_narrow_body(GemmBody body) {
     return body == GemmBody::F32Narrow16 || body == GemmBody::F32Narrow32 || body == GemmBody::F32Narrow16x64 ||
-           body == GemmBody::F32Narrow16x32;
+           body == GemmBody::F32Narrow16x32 || body == GemmBody::F32Narrow64;
 }
 
 inline bool is_f32_body(GemmBody body) {
@@ -104,13 +105,16 @@ inline bool is_f32_body(GemmBody body) {
 }
 
 // A narrow body's tile rows and columns, and its configuration's name in gemm_f32_narrow.h.
-inline int narrow_rows(GemmBody body) { return body == GemmBody::F32Narrow32 ? 32 : 16; }
+inline int narrow_rows(GemmBody body) {
+    return body == GemmBody::F32Narrow64 ? 64 : body == GemmBody::F32Narrow32 ? 32 : 16;
+}
 inline int narrow_cols(GemmBody body) { return body == GemmBody::F32Narrow16x32 ? 32 : 64; }
 inline const char* narrow_config(GemmBody body) {
     switch (body) {
         case GemmBody::F32Narrow16: return "McNarrow16";
         case GemmBody::F32Narrow16x64: return "McNarrow16x64";
         case GemmBody::F32Narrow16x32: return "McNarrow16x32";
+        case GemmBody::F32Narrow64: return "McNarrow64";
         default: return "McNarrow32";
     }
 }

@@ -83,6 +83,9 @@ using McNarrow16 = McNarrowCfg<1, 4, 4, 2, true>;
 using McNarrow32 = McNarrowCfg<2, 4, 4, 2, false>;
 using McNarrow16x64 = McNarrowCfg<1, 4, 4, 2, false>;
 using McNarrow16x32 = McNarrowCfg<1, 2, 4, 2, false>;
+// 64x64 tiles: each operand byte a wave loads feeds 64 MFMAs per 16 k
+// where 32x64 tiles feed 32 per 6 loads (1024^3 as 256 unsplit tiles).
+using McNarrow64 = McNarrowCfg<4, 4, 4, 2, false>;
 
 // One batch of a wave's operands: kU groups of 16 k.
 template <class Cfg>

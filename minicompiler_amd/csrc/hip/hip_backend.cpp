@@ -561,6 +561,7 @@ private:
                     case MCHIP_NARROW_16X64_STREAM: return GemmBody::F32Narrow16;
                     case MCHIP_NARROW_16X64: return GemmBody::F32Narrow16x64;
                     case MCHIP_NARROW_16X32: return GemmBody::F32Narrow16x32;
+                    case MCHIP_NARROW_64X64: return GemmBody::F32Narrow64;
                     default: return GemmBody::F32Narrow32;
                 }
             }

@@ -86,14 +86,15 @@ enum {
     MCHIP_NARROW_16X64_STREAM = 1,  /* 16x64 tiles, B streamed: m <= 16 */
     MCHIP_NARROW_16X64 = 2,         /* 16x64 tiles */
     MCHIP_NARROW_16X32 = 3,         /* 16x32 tiles */
+    MCHIP_NARROW_64X64 = 4,         /* 64x64 tiles */
 };
 int mchip_narrow_rows(int shape);
 int mchip_narrow_cols(int shape);
 
 /* The narrow-tile body, which the split_k rung runs for products whose
  * tiles number at most one per CU. With K <= 2048, a tile shape that gives
- * more than half the CUs a tile runs unsplit (the first of 32x64, 16x64,
- * 16x32 that does); otherwise 32x64 tiles (16x64, B streamed, for m <= 16)
+ * more than half the CUs a tile runs unsplit (the first of 64x64, 32x64,
+ * 16x64, 16x32 that does); otherwise 32x64 tiles (16x64, B streamed, for m <= 16)
  * with K cut into *splits ranges of *k_split (a multiple of 16), at most
  * max_splits of them, so that tiles x ranges stays within the CUs. Its
  * accumulation order is its own (16x16x4 MFMAs, K pieces per wave added

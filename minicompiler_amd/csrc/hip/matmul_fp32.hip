@@ -268,6 +268,7 @@ int launch_narrow(const float* a, const float* b, float* c, int m, int n, int k,
         case MCHIP_NARROW_16X64_STREAM: narrow_kernel<McNarrow16>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
         case MCHIP_NARROW_16X64: narrow_kernel<McNarrow16x64>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
         case MCHIP_NARROW_16X32: narrow_kernel<McNarrow16x32>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
+        case MCHIP_NARROW_64X64: narrow_kernel<McNarrow64>(a, b, c, m, n, k, s, k_split, depth, part, ctr); break;
         default: return hipErrorInvalidValue;
     }
     const hipError_t e = hipGetLastError();
@@ -463,7 +464,7 @@ extern "C" int mchip_f32_unsplit_ring(int m, int n, int k, int splits, int cu_co
 }
 
 extern "C" int mchip_narrow_rows(int shape) {
-    return shape == MCHIP_NARROW_32X64 ? 32 : 16;
+    return shape == MCHIP_NARROW_64X64 ? 64 : shape == MCHIP_NARROW_32X64 ? 32 : 16;
 }
 
 extern "C" int mchip_narrow_cols(int shape) {
@@ -482,12 +483,14 @@ extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu
     // tile runs unsplit, one block per CU with no partials and no sum
     // launch. Measured on an MI355X (launch plus sum, one operand set):
     // 256x512x2048 on 16x32 tiles 9.6 us against 11.2 on 32x64 tiles in 4
-    // ranges; 512^3 on 16x64 tiles 5.4 against 8.3 on 32x64 unsplit. With
+    // ranges; 512^3 on 16x64 tiles 5.4 against 8.3 on 32x64 unsplit;
+    // 1024^3 on 64x64 tiles 19.6 us against 26.7 on the ring in 4 splits
+    // (graph-timed, operands past the MALL). With
     // longer K the smaller tiles' extra operand traffic costs more than a
     // sum launch (256x256x16384: 32.6 us on 16x32 tiles in 2 ranges against
     // 24.8 on 32x64 in 8).
     if (m > 16 && k <= 2048) {
-        for (int sh : {MCHIP_NARROW_32X64, MCHIP_NARROW_16X64, MCHIP_NARROW_16X32}) {
+        for (int sh : {MCHIP_NARROW_64X64, MCHIP_NARROW_32X64, MCHIP_NARROW_16X64, MCHIP_NARROW_16X32}) {
             const long long t = tiles_of(sh);
             if (2 * t > cu_count && t <= cu_count) {
                 *shape = sh;
@@ -497,7 +500,17 @@ extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu
             }
         }
     }
-    const int sh = m <= 16 ? MCHIP_NARROW_16X64_STREAM : MCHIP_NARROW_32X64;
+    // 64x64 tiles when they need at most two K ranges (more than a quarter
+    // of the CUs get a tile), else 32x64: deep K splits of the larger tile
+    // gained nothing. Measured on an MI355X (graph-timed, operands past the
+    // MALL, launch plus sum): 1024x1024x4096 unsplit on 64x64 65.1 us
+    // against 73.7 on the ring (32x64 tiles would number 512);
+    // 128x4096x4096 in 2 ranges 42.3 against 43.6 unsplit on 32x64;
+    // 512x512x8192 in 4 ranges 39.8 against 39.3 in 2; 256x256x16384 in 16
+    // ranges 23.0 against 23.0 in 8.
+    const int sh = m <= 16                                             ? MCHIP_NARROW_16X64_STREAM
+                   : m >= 64 && 4 * tiles_of(MCHIP_NARROW_64X64) > cu_count ? MCHIP_NARROW_64X64
+                                                                           : MCHIP_NARROW_32X64;
     const long long tiles = tiles_of(sh);
     // Measured on an MI355X (one-matmul launches, operands past the MALL):
     // against the ring body, the narrow body wins while its tiles fit one

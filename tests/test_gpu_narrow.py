@@ -1,5 +1,5 @@
-"""The narrow-tile FP32 body (gemm_f32_narrow.h: 16x64 or 32x64 tiles on
-16x16x4 MFMAs, K cut over waves and over ranges of the grid), through the C
+"""The narrow-tile FP32 body (gemm_f32_narrow.h: 16x32, 16x64, 32x64 or 64x64
+tiles on 16x16x4 MFMAs, K cut over waves and over ranges of the grid), through the C
 ABI and in compiled graphs.
 
 It serves split_k products whose tiles number at most one per CU, so its
@@ -24,10 +24,13 @@ GUARD = 4096
 # 512^3 and 200x512x640 (ragged M) on 16x64 tiles, unsplit. Waves with 32
 # groups of K or more load two groups per batch (256x2048x512 on 16x32
 # tiles, 256x256x16384 in 8 ranges), and 64x2064x260 gives them 33 (an odd
-# count: a last group on its own).
+# count: a last group on its own). 64x64 tiles: 1024^3 unsplit, 1000x528x1000
+# unsplit with ragged edges, 128x4096x4096 and 300x4112x1000 (ragged) in 2
+# K ranges.
 SHAPES = [(1, 16, 4, 1), (5, 96, 260, 3), (16, 4096, 4096, 8), (33, 1040, 1000, 4), (300, 96, 260, 2),
           (256, 512, 2048, 8), (256, 2048, 512, 32), (512, 512, 512, 8), (16, 64, 68, 64), (256, 16384, 256, 64),
-          (200, 512, 640, 4), (64, 2064, 260, 1)]
+          (200, 512, 640, 4), (64, 2064, 260, 1), (1024, 1024, 1024, 4), (1000, 528, 1000, 4), (128, 4096, 4096, 8),
+          (300, 4112, 1000, 4)]
 
 
 def run(mc, ring, a, b, m, k, n, splits):
@@ -63,11 +66,12 @@ def test_narrow_split_k_is_within_the_dot_product_bound_and_deterministic(device
 
 
 def test_the_plan_takes_narrow_tiles_only_where_they_fit_one_per_cu(device, mc, oracle):
-    # 256x2048x512 (256 tiles of 32x64) and 16x4096x4096 (64 of 16x64) run
-    # narrow; 1024x1024x1024 (512 tiles) keeps the ring. The plan's split_k
-    # launch then equals the forced narrow launch (same plan) bit for bit,
-    # or the forced wide ring's.
-    for (m, k, n), body in (((256, 512, 2048), "narrow"), ((16, 4096, 4096), "narrow"), ((1024, 1024, 1024), "wide")):
+    # 256x2048x512 (256 tiles of 32x64), 16x4096x4096 (64 of 16x64) and
+    # 1024x1024x1024 (256 of 64x64) run narrow; 1024x2048x2048 (512 tiles of
+    # 64x64) keeps the ring, in 2 splits. The plan's split_k launch then equals the forced
+    # narrow launch (same plan) bit for bit, or the forced wide8 ring's.
+    for (m, k, n), body in (((256, 512, 2048), "narrow"), ((16, 4096, 4096), "narrow"),
+                            ((1024, 1024, 1024), "narrow"), ((1024, 2048, 2048), "wide8")):
         print(f"case plan {m}x{k}x{n} -> {body}", flush=True)
         a = oracle.uniform(m * k, 41, -1.0, 1.0)
         b = oracle.uniform(k * n, 42, -1.0, 1.0)
@@ -86,7 +90,8 @@ def test_a_forced_narrow_launch_the_product_cannot_take_is_an_error(device, mc):
 
 
 GRAPHS = [("mlp_gelu", {"B": 256}), ("mlp_gelu", {"B": 16}), ("matmul_bias_relu", {"M": 16, "K": 1024, "N": 1000}),
-          ("matmul_bias_relu", {"M": 96, "K": 512, "N": 512}), ("matmul_bias_relu", {"M": 512, "K": 512, "N": 512})]
+          ("matmul_bias_relu", {"M": 96, "K": 512, "N": 512}), ("matmul_bias_relu", {"M": 512, "K": 512, "N": 512}),
+          ("matmul_bias_relu", {"M": 1024, "K": 1024, "N": 1024})]
 
 
 @pytest.mark.parametrize("name,dims", GRAPHS)
@@ -111,7 +116,8 @@ def test_graphs_on_narrow_tiles_fuse_their_groups_bit_for_bit_and_match_the_orac
 
 def test_short_k_products_run_on_the_tile_shape_that_gives_most_cus_a_tile(device, mc):
     # On 256 CUs: the MLP at B=256 runs GEMM1 (256x2048x512) on 32x64 tiles
-    # and GEMM2 (256x512x2048) on 16x32 tiles, 512^3 on 16x64 tiles.
+    # and GEMM2 (256x512x2048) on 16x32 tiles, 512^3 on 16x64 tiles, 1024^3
+    # on 64x64 tiles.
     if int(device["cu_count"]) != 256:
         pytest.skip("tile counts are for 256 CUs")
     opts = {"matmul": "split_k"}
@@ -120,3 +126,6 @@ def test_short_k_products_run_on_the_tile_shape_that_gives_most_cus_a_tile(devic
     sq = "\n".join(mc.Compiled(path=mc.graph_path("matmul_bias_relu"), dims={"M": 512, "K": 512, "N": 512},
                                options=opts).kernel_sources)
     assert "mc_gemm_f32_narrow<McNarrow16x64>" in sq
+    big = "\n".join(mc.Compiled(path=mc.graph_path("matmul_bias_relu"), dims={"M": 1024, "K": 1024, "N": 1024},
+                                options=opts).kernel_sources)
+    assert "mc_gemm_f32_narrow<McNarrow64>" in big

@@ -65,12 +65,16 @@ struct McNarrowVec<2> {
 // (tiles of 16 kVec columns), kW waves, up to kU groups of 16 k per batch of
 // loads; kStreamB: B is read by one tile row only (M <= 16), so its loads
 // are non-temporal (a read-only stream reached 7.1 TB/s with them against
-// 6.3 TB/s without on an MI355X).
-template <int kRG_, int kVec_, int kW_, int kU_, bool kStreamB_>
+// 6.3 TB/s without on an MI355X). kRedRows: rows of the LDS array the waves
+// add their tiles through (at least kRows); more than kRows only to keep a
+// second block off the CU (LDS is 160 KiB per CU).
+template <int kRG_, int kVec_, int kW_, int kU_, bool kStreamB_, int kRedRows_ = 16 * kRG_>
 struct McNarrowCfg {
     static constexpr int kRG = kRG_, kVec = kVec_, kW = kW_, kU = kU_;
     static constexpr bool kStreamB = kStreamB_;
     static constexpr int kRows = 16 * kRG, kCols = 16 * kVec, kThreads = 64 * kW;
+    static constexpr int kRedRows = kRedRows_;
+    static_assert(kRedRows >= kRows, "the reduction holds a whole tile");
 };
 
 // The configurations the library runs, 4 waves each, batches of up to 2
@@ -84,8 +88,11 @@ using McNarrow32 = McNarrowCfg<2, 4, 4, 2, false>;
 using McNarrow16x64 = McNarrowCfg<1, 4, 4, 2, false>;
 using McNarrow16x32 = McNarrowCfg<1, 2, 4, 2, false>;
 // 64x64 tiles: each operand byte a wave loads feeds 64 MFMAs per 16 k
-// where 32x64 tiles feed 32 per 6 loads (1024^3 as 256 unsplit tiles).
-using McNarrow64 = McNarrowCfg<4, 4, 4, 2, false>;
+// where 32x64 tiles feed 32 per 6 loads (1024^3 as 256 unsplit tiles). One
+// block per CU: its 96 KiB reduction array leaves no room for a second.
+// With 512 tiles (two per CU, 1024x2048x512) two co-resident blocks took
+// 31-36 us against 22.5 us for one block per CU in two rounds.
+using McNarrow64 = McNarrowCfg<4, 4, 4, 2, false, 96>;
 
 // One batch of a wave's operands: kU groups of 16 k.
 template <class Cfg>
@@ -106,7 +113,7 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
                                                    const Epilogue& epilogue) {
     constexpr int kRG = Cfg::kRG, kW = Cfg::kW, kVec = Cfg::kVec, kU = Cfg::kU;
     typedef typename McNarrowVec<kVec>::type BV;
-    __shared__ BV red[kW][Cfg::kRows][16];  // [wave][row][column chunk]
+    __shared__ BV red[kW][Cfg::kRedRows][16];  // [wave][row][column chunk]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
     const int s = lane >> 4, cl = lane & 15;
@@ -247,27 +254,44 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     // this launch adds go out as device-scope stores (mc_split_store).
     const bool fold = raw && counters != nullptr;
     const bool vec_out = (reinterpret_cast<unsigned long long>(out) & (sizeof(BV) - 1)) == 0;
-    for (int t = threadIdx.x; t < Cfg::kRows * 16; t += Cfg::kThreads) {
+    // A lane's chunks (kRows 16 / kThreads of them, 1 to 4): all summed and
+    // through the epilogue before the first store, so the epilogue's operand
+    // loads of every chunk are in flight together (chunk by chunk, each
+    // chunk's store waited for its own loads: the MLP's GEMM1 + bias + GELU
+    // at B=1024 on 64x64 tiles took 31.4 us against 22.6 for the bare GEMM).
+    constexpr int kChunks = Cfg::kRows * 16 / Cfg::kThreads;
+    static_assert(kChunks * Cfg::kThreads == Cfg::kRows * 16, "a whole number of chunks per lane");
+    BV sums[kChunks];
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int t = static_cast<int>(threadIdx.x) + i * Cfg::kThreads;
         const int r = t >> 4, ch = t & 15;
         BV sum = red[0][r][ch];
 #pragma unroll
         for (int w = 1; w < kW; ++w) sum += red[w][r][ch];
         const int row = row0 + r, col = col0 + kVec * ch;
-        if (row < m && col < n) {
+        if (!raw && row < m && col < n) {
             const long long at = static_cast<long long>(row) * n + col;
-            if (!raw) {
 #pragma unroll
-                for (int j = 0; j < kVec; ++j) sum[j] = epilogue(sum[j], static_cast<unsigned>(at + j));
-            }
-            if (fold) {
+            for (int j = 0; j < kVec; ++j) sum[j] = epilogue(sum[j], static_cast<unsigned>(at + j));
+        }
+        sums[i] = sum;
+    }
 #pragma unroll
-                for (int j = 0; j < kVec; ++j) mc_split_store(out + at + j, sum[j]);
-            } else if (vec_out) {
-                *reinterpret_cast<BV*>(out + at) = sum;
-            } else {
+    for (int i = 0; i < kChunks; ++i) {
+        const int t = static_cast<int>(threadIdx.x) + i * Cfg::kThreads;
+        const int r = t >> 4, ch = t & 15;
+        const int row = row0 + r, col = col0 + kVec * ch;
+        if (row >= m || col >= n) continue;
+        const long long at = static_cast<long long>(row) * n + col;
+        if (fold) {
 #pragma unroll
-                for (int j = 0; j < kVec; ++j) out[at + j] = sum[j];
-            }
+            for (int j = 0; j < kVec; ++j) mc_split_store(out + at + j, sums[i][j]);
+        } else if (vec_out) {
+            *reinterpret_cast<BV*>(out + at) = sums[i];
+        } else {
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) out[at + j] = sums[i][j];
         }
     }
     if (!fold) return;

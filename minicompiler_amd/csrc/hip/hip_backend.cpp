@@ -566,15 +566,7 @@ private:
                 }
             }
         }
-        if (l.matmul == MatmulKernel::SplitK && l.ring_cfg == MCHIP_RING_NONE &&
-            mchip_f32_unsplit_ring(l.m, l.n, l.k, l.splits, device_.cu_count)) {
-            // As the split_k rung does: unsplit on 64x128 ring tiles.
-            l.ring_cfg = MCHIP_RING_MID;
-            l.k_split = l.k;
-            l.depth = 1;
-        } else {
-            split_layout(l.k, l.splits, &l.k_split, &l.depth);
-        }
+        split_layout(l.k, l.splits, &l.k_split, &l.depth);
         if (l.matmul == MatmulKernel::Vectorized || l.k % 4 != 0) return GemmBody::F32Mfma;
         unsigned grid = 0, block = 0;
         switch (mchip_f32_ring_plan_cfg(l.m, l.n, l.k, l.depth, device_.cu_count, l.ring_cfg, &grid, &block)) {

@@ -73,12 +73,6 @@ enum {
 int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count, unsigned* grid, unsigned* block);
 int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_count, int cfg, unsigned* grid, unsigned* block);
 
-/* 1 when a split_k product asked to split K (splits > 1) runs faster
- * unsplit on the ring's 64x128 tiles (MCHIP_RING_MID): K <= 1024 and those
- * tiles number more than half the CUs and at most all of them. The split_k
- * rung then does so (when A, B and C are 16-byte aligned and the caller
- * forces no configuration), in place of the split rule's count. */
-int mchip_f32_unsplit_ring(int m, int n, int k, int splits, int cu_count);
 
 /* The narrow-tile body (gemm_f32_narrow.h) in its tile shapes. */
 enum {
@@ -92,9 +86,9 @@ int mchip_narrow_rows(int shape);
 int mchip_narrow_cols(int shape);
 
 /* The narrow-tile body, which the split_k rung runs for products whose
- * tiles number at most one per CU. With K <= 2048, a tile shape that gives
- * more than half the CUs a tile runs unsplit (the first of 64x64, 32x64,
- * 16x64, 16x32 that does); otherwise 32x64 tiles (16x64, B streamed, for m <= 16)
+ * tiles number at most one per CU (two for 64x64 tiles). With K <= 2048, a
+ * tile shape that gives more than half the CUs a tile runs unsplit (the
+ * first of 64x64, 32x64, 16x64, 16x32 that does); otherwise 32x64 tiles (16x64, B streamed, for m <= 16)
  * with K cut into *splits ranges of *k_split (a multiple of 16), at most
  * max_splits of them, so that tiles x ranges stays within the CUs. Its
  * accumulation order is its own (16x16x4 MFMAs, K pieces per wave added

@@ -313,11 +313,6 @@ MfmaPlan plan_mfma_f32(bool double_buffer, bool a16, bool b16, bool c16, bool ws
         p.status = hipErrorInvalidValue;
         return p;
     }
-    if (split_k && ring_cfg == MCHIP_RING_NONE && a16 && b16 && c16 &&
-        mchip_f32_unsplit_ring(m, n, k, splits, device_cu_count())) {
-        splits = 1;
-        ring_cfg = MCHIP_RING_MID;
-    }
     p.k_split = split_len(k, splits, kMBK);
     p.depth = std::max(1, (k + p.k_split - 1) / p.k_split);
     if (p.depth > 1 && !has_ws) {
@@ -450,19 +445,6 @@ extern "C" int mchip_f32_ring_plan(int m, int n, int k, int depth, int cu_count,
     return mchip_f32_ring_plan_cfg(m, n, k, depth, cu_count, MCHIP_RING_NONE, grid, block);
 }
 
-extern "C" int mchip_f32_unsplit_ring(int m, int n, int k, int splits, int cu_count) {
-    // Measured on an MI355X (same process, operands past the MALL, graph-timed
-    // launch plus sum): 1024x2048x512 unsplit on 64x128 tiles 24.2 us against
-    // 28.7 us for the rule's 2 splits on 128x128 tiles; 2048x1024x512 24.2
-    // against 28.6; 768x2048x512 23.8 against 27.4; 1024x2048x1024 43.6
-    // against 44.7. Where 64x128 tiles leave half the CUs idle, or K is
-    // longer, the split wins (1024^3: 42.8 against 28.0; 1024x1024x4096:
-    // 160.3 against 75.9).
-    if (splits < 2 || cu_count < 1 || m < 1 || n % 4 != 0 || k % 32 != 0 || k > 1024) return 0;
-    const long long tiles = static_cast<long long>((m + 63) / 64) * ((n + 127) / 128);
-    return 2 * tiles > cu_count && tiles <= cu_count ? 1 : 0;
-}
-
 extern "C" int mchip_narrow_rows(int shape) {
     return shape == MCHIP_NARROW_64X64 ? 64 : shape == MCHIP_NARROW_32X64 ? 32 : 16;
 }
@@ -489,10 +471,16 @@ extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu
     // longer K the smaller tiles' extra operand traffic costs more than a
     // sum launch (256x256x16384: 32.6 us on 16x32 tiles in 2 ranges against
     // 24.8 on 32x64 in 8).
+    // 64x64 tiles also run two per CU (in two rounds of one block per CU):
+    // 1024x2048x512 22.6 us against 24.2 on the ring unsplit,
+    // 1024x2048x1024 38.9 against 44.2 in 2 splits, 512x4096x1024 43.0
+    // against 44.5; at four per CU the ring wins (2048x2048x512: 44.3
+    // against 38.2).
     if (m > 16 && k <= 2048) {
         for (int sh : {MCHIP_NARROW_64X64, MCHIP_NARROW_32X64, MCHIP_NARROW_16X64, MCHIP_NARROW_16X32}) {
             const long long t = tiles_of(sh);
-            if (2 * t > cu_count && t <= cu_count) {
+            const long long per_cu = sh == MCHIP_NARROW_64X64 ? 2 : 1;
+            if (2 * t > cu_count && t <= per_cu * cu_count) {
                 *shape = sh;
                 *k_split = k;
                 *splits = 1;

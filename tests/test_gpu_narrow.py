@@ -65,13 +65,13 @@ def test_narrow_split_k_is_within_the_dot_product_bound_and_deterministic(device
     assert not np.any(bad), f"{np.count_nonzero(bad)} elements outside the bound"
 
 
-def test_the_plan_takes_narrow_tiles_only_where_they_fit_one_per_cu(device, mc, oracle):
+def test_the_plan_takes_narrow_tiles_only_where_they_fit(device, mc, oracle):
     # 256x2048x512 (256 tiles of 32x64), 16x4096x4096 (64 of 16x64) and
-    # 1024x1024x1024 (256 of 64x64) run narrow; 1024x2048x2048 (512 tiles of
-    # 64x64) keeps the ring, in 2 splits. The plan's split_k launch then equals the forced
+    # 1024x1024x1024 (256 of 64x64) run narrow; 1024x4096x2048 (K past 2048,
+    # 512 tiles of 64x64) keeps the ring, in 2 splits. The plan's split_k launch then equals the forced
     # narrow launch (same plan) bit for bit, or the forced wide8 ring's.
     for (m, k, n), body in (((256, 512, 2048), "narrow"), ((16, 4096, 4096), "narrow"),
-                            ((1024, 1024, 1024), "narrow"), ((1024, 2048, 2048), "wide8")):
+                            ((1024, 1024, 1024), "narrow"), ((1024, 4096, 2048), "wide8")):
         print(f"case plan {m}x{k}x{n} -> {body}", flush=True)
         a = oracle.uniform(m * k, 41, -1.0, 1.0)
         b = oracle.uniform(k * n, 42, -1.0, 1.0)
@@ -129,3 +129,6 @@ def test_short_k_products_run_on_the_tile_shape_that_gives_most_cus_a_tile(devic
     big = "\n".join(mc.Compiled(path=mc.graph_path("matmul_bias_relu"), dims={"M": 1024, "K": 1024, "N": 1024},
                                 options=opts).kernel_sources)
     assert "mc_gemm_f32_narrow<McNarrow64>" in big
+    # The MLP at B=1024: GEMM1 (1024x2048x512) on 64x64 tiles, two per CU.
+    mlp = "\n".join(mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": 1024}, options=opts).kernel_sources)
+    assert "mc_gemm_f32_narrow<McNarrow64>" in mlp

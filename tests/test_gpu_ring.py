@@ -117,11 +117,12 @@ def test_forced_ring_configurations_give_the_plans_bits(device, mc, oracle, m, k
     assert np.all(np.abs(planned.astype(np.float64) - exact) <= bound)
 
 
-def test_split_k_runs_unsplit_on_64x128_tiles_where_they_fill_the_cus(device, mc, oracle):
-    # 1024x512x2048 (m, k, n): the split rule asks for 2 splits on 256 CUs; 64x128
-    # tiles number 256, so the split_k rung runs it unsplit on the mid
-    # configuration: the bits of a forced mid launch with one split (not
-    # those of the rule's two), within the dot-product bound.
+def test_split_k_runs_unsplit_on_two_64x64_narrow_tiles_per_cu_where_they_fit(device, mc, oracle):
+    # 1024x512x2048 (m, k, n): the split rule asks for 2 splits on 256 CUs;
+    # 64x64 narrow tiles number 512, two per CU, so the split_k rung runs it
+    # unsplit on them: the bits of a forced narrow launch (the same plan),
+    # not those of the rule's two splits on the ring, within the dot-product
+    # bound.
     m, k, n = 1024, 512, 2048
     if int(device["cu_count"]) != 256:
         pytest.skip("tile counts are for 256 CUs")
@@ -132,8 +133,8 @@ def test_split_k_runs_unsplit_on_64x128_tiles_where_they_fill_the_cus(device, mc
     da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
     ws = mc.DeviceBuffer(mc.matmul_workspace_bytes("split_k", m, n, splits))
     planned = run_cfg(mc, "split_k", "auto", da, db, m, n, k, splits, ws)
-    unsplit = run_cfg(mc, "split_k", "mid", da, db, m, n, k, 1, None)
-    assert np.array_equal(planned.view(np.uint32), unsplit.view(np.uint32))
+    narrow = run_cfg(mc, "split_k", "narrow", da, db, m, n, k, splits, ws)
+    assert np.array_equal(planned.view(np.uint32), narrow.view(np.uint32))
     split = run_cfg(mc, "split_k", "wide", da, db, m, n, k, splits, ws)
     assert not np.array_equal(planned.view(np.uint32), split.view(np.uint32))
     rows = np.arange(0, m, 7)

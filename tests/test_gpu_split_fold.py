@@ -22,10 +22,10 @@ FOLDED = "summed in the GEMM"
 
 # (m, k, n, options). The bench's split shapes: 16x4096x4096 (streamed
 # 16x64 tiles, 4 K ranges), 256x256x16384 (32x64 tiles, 8 ranges);
-# 1024x2048x2048 (the wide8 ring, 2 splits); 128x4096x4096 (64x64 tiles,
+# 1024x4096x2048 (the wide8 ring, 2 splits); 128x4096x4096 (64x64 tiles,
 # 2 ranges); ragged M and N on 32x64 tiles; each ring
 # configuration forced with a deep split, ragged where it can be.
-CASES = [(16, 4096, 4096, {}), (256, 16384, 256, {}), (1024, 2048, 2048, {}), (128, 4096, 4096, {}),
+CASES = [(16, 4096, 4096, {}), (256, 16384, 256, {}), (1024, 4096, 2048, {}), (128, 4096, 4096, {}),
          (33, 1040, 1000, {}),
          (512, 4096, 512, {"ring": "wide"}), (200, 4096, 516, {"ring": "mid"}), (32, 4096, 2048, {"ring": "thin"}),
          (300, 8192, 300, {"ring": "big"})]
@@ -69,7 +69,7 @@ def test_splits_added_in_the_launch_equal_the_separate_sum(device, mc, oracle, m
 # store of each tile: on streamed 16x64 tiles, on the wide ring, on the mid
 # ring with ragged edges, and the MLP at a small batch (both GEMMs split).
 FUSED = [("matmul_bias_relu", {"M": 16, "K": 4096, "N": 4096}, {}),
-         ("matmul_bias_relu", {"M": 1024, "K": 2048, "N": 2048}, {}),
+         ("matmul_bias_relu", {"M": 1024, "K": 4096, "N": 2048}, {}),
          ("matmul_bias_relu", {"M": 200, "K": 4096, "N": 516}, {"ring": "mid"}),
          ("mlp_gelu", {"B": 16}, {})]
 

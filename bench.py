@@ -34,10 +34,11 @@ other BASELINE configs measured in the same process (skip with --quick),
 each with a `cpu_baseline`: the CPU oracle (a C++ restatement of the
 reference's Eigen backend, test infrastructure) on a bounded row sample of
 that workload on this host, one thread (the reference's configuration) and
-the host's CPU share. `device.clocks` summarises the engine clock sampled
-(AMD SMI) while the headline workload ran on the GPU (its warm-up, per-launch
-timings and timed steps), `device.clocks_timed_steps` the samples taken during
-the timed steps alone.
+the host's CPU share. `device.clocks` summarises the engine clock (AMD SMI)
+while the headline workload ran on the GPU (its warm-up, per-launch timings
+and timed steps), one value per firmware snapshot of the metrics table (about
+one a second), `device.clocks_timed_steps` the snapshots seen during the
+timed steps alone.
 """
 
 from __future__ import annotations
@@ -137,21 +138,32 @@ def warm_up_for(seconds: float, batch) -> int:
 
 
 class ClockSampler:
-    """Samples the engine clock (AMD SMI, mc_gpu_sm_clock_mhz) every few
+    """Samples the engine clock (AMD SMI, mc_gpu_clock_sample) every few
     milliseconds on a thread while active, as the reference records the SM
-    clock range of a run (bench/harness.hpp:264-279)."""
+    clock range of a run (bench/harness.hpp:264-279). AMD SMI's value is the
+    power-management firmware's snapshot, refreshed about once a second: the
+    summary keeps one value per snapshot (by its firmware timestamp), and
+    counts the reads apart. A window shorter than the refresh period may see
+    no snapshot taken inside it."""
 
     def __init__(self, mc, period_s: float = 0.002):
-        self.mc, self.period, self.samples = mc, period_s, []
+        self.mc, self.period = mc, period_s
+        self.reads = 0
+        self.snapshots: dict[int, float] = {}  # firmware timestamp (ns) -> MHz
+        self.samples: list[float] = []  # one per snapshot, in order
         self._stop = threading.Event()
         self._thread = None
 
     def __enter__(self):
         def run():
             while not self._stop.is_set():
-                v = self.mc.gpu_clock_mhz()
+                v, stamp = self.mc.gpu_clock_sample()
                 if v > 0:
-                    self.samples.append(v)
+                    self.reads += 1
+                    key = stamp if stamp else -self.reads  # no timestamp: every read counts
+                    if key not in self.snapshots:
+                        self.snapshots[key] = v
+                        self.samples.append(v)
                 self._stop.wait(self.period)
         self._thread = threading.Thread(target=run, daemon=True)
         self._thread.start()
@@ -165,12 +177,18 @@ class ClockSampler:
         x = sorted(self.samples)
         return x[len(x) // 2] if x else 0.0
 
+    def refresh_s(self) -> float | None:
+        """Median spacing of the snapshots' firmware timestamps, in seconds."""
+        stamps = sorted(k for k in self.snapshots if k > 0)
+        gaps = sorted(b - a for a, b in zip(stamps, stamps[1:]))
+        return gaps[len(gaps) // 2] / 1e9 if gaps else None
+
     def summary(self) -> dict:
         x = self.samples
         if not x:
-            return {"samples": 0}
-        return {"samples": len(x), "min_mhz": min(x), "median_mhz": self.median(), "mean_mhz": sum(x) / len(x),
-                "max_mhz": max(x)}
+            return {"samples": 0, "reads": self.reads}
+        return {"samples": len(x), "reads": self.reads, "min_mhz": min(x), "median_mhz": self.median(),
+                "mean_mhz": sum(x) / len(x), "max_mhz": max(x), "snapshot_refresh_s": self.refresh_s()}
 
 
 def rotation_sets(set_bytes: int) -> int:
@@ -848,9 +866,10 @@ def main() -> int:
         line["roofline"]["traffic"] = measured_traffic(line["config"]["workload"], line["roofline"]["kernel"])
     d = mc.device_json(headline_run.samples)
     line["device"] = {k: d[k] for k in ("name", "arch", "cu_count", "clock_mhz", "mem_clock_mhz", "bus_width_bits")}
-    line["device"]["clocks"] = {**d["clocks"], "median_mhz": headline_run.median(),
+    line["device"]["clocks"] = {**headline_run.summary(),
                                 "during": "the headline workload's GPU work (warm-up, per-launch timings, timed steps)",
-                                "source": "AMD SMI current GFX clock (mean over XCDs), sampled every 2 ms"}
+                                "source": "AMD SMI current GFX clock (mean over XCDs), read every 2 ms; one value per "
+                                          "firmware snapshot (the metrics table is refreshed about once a second)"}
     line["device"]["clocks_timed_steps"] = {**sampler.summary(), "during": "the headline's timed steps only"}
     line["device"]["clocks_configs"] = {**whole.summary(), "during": "the other configs' GPU work",
                                         "period_ms": 50}

@@ -148,8 +148,13 @@ struct DeviceInfo {
 
 Result<DeviceInfo> query_device(int device = 0);
 
-// The engine clock right now in MHz, or 0 when the runtime cannot tell.
+// The engine clock in MHz at the power-management firmware's last refresh
+// of its metrics (about once a second), or 0 when the runtime cannot tell.
 double current_clock_mhz(int device = 0);
+// The same, with the refresh's firmware timestamp in ns (0 when the source
+// has none): reads with the same stamp are the same snapshot. False, with 0
+// MHz, when the clock cannot be read.
+bool current_clock_sample(int device, double* mhz, unsigned long long* stamp_ns);
 
 // A graph compiled for the GPU. Every device allocation is one arena taken at
 // compile time: pooled intermediates and outputs at the memory plan's

@@ -59,10 +59,16 @@ MC_API int mc_kernel_launches(void* handle);
 /* The matmul kernel of each matmul, comma-separated, truncated to `size`.
  * Returns 0, or 1 without an executable (not a length: capi.cpp:184-202). */
 MC_API int mc_matmul_kernels(void* handle, char* out, int size);
-/* The engine clock right now in MHz (AMD SMI's current GFX clock of device
- * 0; the reference reads NVML's SM clock), 0 when it cannot be read.
+/* The engine clock in MHz (AMD SMI's current GFX clock of device 0; the
+ * reference reads NVML's SM clock), 0 when it cannot be read. AMD SMI's
+ * value is the firmware's snapshot, refreshed about once a second.
  * (capi.cpp:204-210) */
 MC_API double mc_gpu_sm_clock_mhz(void);
+/* mc_gpu_sm_clock_mhz with the snapshot's firmware timestamp in ns (0 when
+ * the source has none), so that a sampler keeps one value per snapshot.
+ * 0 ok, 1 the clock cannot be read (*mhz = 0). The reference's sampler
+ * reads NVML's clock alone (device_info.cpp:14-31, harness.hpp:264-279). */
+MC_API int mc_gpu_clock_sample(double* mhz, unsigned long long* stamp_ns);
 /* JSON description of device 0 (name, arch, CUs, clocks, bus, peaks) with the
  * `clocks` samples summarised. 0 ok, 1 no device, 2 `out` too small.
  * (capi.cpp:215-231) */

@@ -68,6 +68,7 @@ _SIGNATURES = {
     "mc_kernel_launches": (_i, [_vp]),
     "mc_matmul_kernels": (_i, [_vp, _cp, _i]),
     "mc_gpu_sm_clock_mhz": (_d, []),
+    "mc_gpu_clock_sample": (_i, [_c.POINTER(_d), _c.POINTER(_c.c_ulonglong)]),
     "mc_gpu_device_json": (_i, [_c.POINTER(_d), _i, _cp, _i]),
     "mc_release": (None, [_vp]),
     "mc_last_error": (_i, [_cp, _i]),
@@ -314,8 +315,18 @@ class CapturedGraph:
 
 
 def gpu_clock_mhz() -> float:
-    """The engine clock of device 0 right now (AMD SMI), 0 if unreadable."""
+    """The engine clock of device 0 (AMD SMI's snapshot, refreshed about once
+    a second), 0 if unreadable."""
     return float(library().mc_gpu_sm_clock_mhz())
+
+
+def gpu_clock_sample() -> tuple[float, int]:
+    """(MHz, firmware timestamp in ns of the snapshot) for device 0; (0, 0)
+    if unreadable. Reads with the same timestamp are one snapshot."""
+    mhz, stamp = ctypes.c_double(), ctypes.c_ulonglong()
+    if library().mc_gpu_clock_sample(ctypes.byref(mhz), ctypes.byref(stamp)) != 0:
+        return 0.0, 0
+    return float(mhz.value), int(stamp.value)
 
 
 def _stream_handle(stream):

@@ -480,6 +480,15 @@ MC_API int mc_matmul_kernels(void* h, char* out, int size) {
 
 MC_API double mc_gpu_sm_clock_mhz(void) { return hip::current_clock_mhz(0); }
 
+MC_API int mc_gpu_clock_sample(double* mhz, unsigned long long* stamp_ns) {
+    double v = 0.0;
+    unsigned long long t = 0;
+    const bool ok = hip::current_clock_sample(0, &v, &t);
+    if (mhz) *mhz = v;
+    if (stamp_ns) *stamp_ns = t;
+    return ok ? 0 : 1;
+}
+
 MC_API int mc_gpu_device_json(const double* clocks, int n, char* out, int size) {
     Result<hip::DeviceInfo> d = hip::query_device(0);
     if (!d.ok()) return 1;

@@ -11,6 +11,13 @@
 // way). The value is the gpu_metrics table's current GFX clock: the mean of
 // the per-XCC current clocks when the table has them (MI300-class parts),
 // else its single current clock, else the 1-second average AMD SMI reports.
+//
+// The power-management firmware refreshes that table about once a second
+// (on an MI355X its timestamp advanced in steps of 1.000 s, and AMD SMI's
+// clock query returned the same snapshot): a read is the clock at the last
+// refresh, not at the moment of the call. current_clock_sample also returns
+// the snapshot's firmware timestamp, so a caller can keep one value per
+// snapshot.
 
 #include "hip_rt.h"
 #include "minicompiler/hip/hip_backend.hpp"
@@ -84,9 +91,11 @@ bool valid_mhz(unsigned v) { return v != 0 && v != 0xFFFF; }
 
 }  // namespace
 
-double current_clock_mhz(int device) {
+bool current_clock_sample(int device, double* mhz, unsigned long long* stamp_ns) {
+    *mhz = 0.0;
+    *stamp_ns = 0;
     amdsmi_processor_handle h = nullptr;
-    if (!processor_of(device, &h)) return 0.0;
+    if (!processor_of(device, &h)) return false;
     const AmdSmi& smi = amdsmi();
     if (smi.metrics) {
         amdsmi_gpu_metrics_t m{};
@@ -99,15 +108,33 @@ double current_clock_mhz(int device) {
                     ++n;
                 }
             }
-            if (n > 0) return sum / n;
-            if (valid_mhz(m.current_gfxclk)) return m.current_gfxclk;
+            *stamp_ns = static_cast<unsigned long long>(m.firmware_timestamp) * 10;  // 10 ns units
+            if (n > 0) {
+                *mhz = sum / n;
+                return true;
+            }
+            if (valid_mhz(m.current_gfxclk)) {
+                *mhz = m.current_gfxclk;
+                return true;
+            }
+            *stamp_ns = 0;
         }
     }
     if (smi.clock_info) {
         amdsmi_clk_info_t info{};
-        if (smi.clock_info(h, AMDSMI_CLK_TYPE_GFX, &info) == AMDSMI_STATUS_SUCCESS && info.clk > 0) return info.clk;
+        if (smi.clock_info(h, AMDSMI_CLK_TYPE_GFX, &info) == AMDSMI_STATUS_SUCCESS && info.clk > 0) {
+            *mhz = info.clk;
+            return true;
+        }
     }
-    return 0.0;
+    return false;
+}
+
+double current_clock_mhz(int device) {
+    double mhz = 0.0;
+    unsigned long long stamp = 0;
+    current_clock_sample(device, &mhz, &stamp);
+    return mhz;
 }
 
 }  // namespace minicompiler::hip

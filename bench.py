@@ -782,8 +782,8 @@ def main() -> int:
     MIN_TIMED_MS = args.min_timed_ms
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU; the multi-GPU sharding is a design only "
-              "(see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU (rows of each GEMM and elementwise group would shard "
+              "across GPUs with no exchange, which is not built). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     import minicompiler_amd as mc

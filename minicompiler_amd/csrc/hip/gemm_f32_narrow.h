@@ -256,9 +256,10 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     const bool vec_out = (reinterpret_cast<unsigned long long>(out) & (sizeof(BV) - 1)) == 0;
     // A lane's chunks (kRows 16 / kThreads of them, 1 to 4): all summed and
     // through the epilogue before the first store, so the epilogue's operand
-    // loads of every chunk are in flight together (chunk by chunk, each
-    // chunk's store waited for its own loads: the MLP's GEMM1 + bias + GELU
-    // at B=1024 on 64x64 tiles took 31.4 us against 22.6 for the bare GEMM).
+    // loads of every chunk are in flight together, and a per-column operand
+    // (a bias: every chunk of a lane is in the same columns) is loaded once;
+    // chunk by chunk, the compiler loaded it again and waited for it in each
+    // chunk, after the previous chunk's store.
     constexpr int kChunks = Cfg::kRows * 16 / Cfg::kThreads;
     static_assert(kChunks * Cfg::kThreads == Cfg::kRows * 16, "a whole number of chunks per lane");
     BV sums[kChunks];

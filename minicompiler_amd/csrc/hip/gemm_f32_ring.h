@@ -316,10 +316,10 @@ __device__ __forceinline__ void mc_ring_barrier() {
 // With one or two columns per lane (every configuration but big) the
 // epilogue runs over a batch of rows (32 or 64 values) before the batch's
 // first store: with each row stored right after its epilogue, the compiler
-// waited for the epilogue's operand loads a few rows at a time and loaded a
-// per-column operand (a bias) again for every row; batched, a row's adjacent
-// operand elements merge into one load and the batch's loads are in flight
-// before one wait. The MLP's GEMM2 with b2 + residual (wide): 139.2-139.6 us
+// waited for the epilogue's operand loads a few rows at a time (9 waits per
+// tile of the MLP's GEMM2); batched, a row's two residual floats merge into
+// one 8-byte load and the batch's loads are in flight before one wait (2
+// waits per tile). The MLP's GEMM2 with b2 + residual (wide): 139.2-139.6 us
 // against 140.8-141.1. Big keeps each row's store right after its epilogue
 // (its 4 columns per lane already load a bias once): batched, its GEMM with
 // bias + GELU took 136.5-136.7 us against 135.3 (one MI355X, 3 runs each).
@@ -375,9 +375,8 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
                     o[di][v] = typename BV::type{};
                     continue;
                 }
-                // The epilogue's element index, in the 32 bits it takes:
-                // a periodic operand's index (a bias at i % N) then folds to
-                // the column, loaded once for every row.
+                // The epilogue's element index, computed in the 32 bits it
+                // takes (the same value as the 64-bit offset truncated).
                 const unsigned at = static_cast<unsigned>(row) * static_cast<unsigned>(n) + static_cast<unsigned>(col);
 #pragma unroll
                 for (int j = 0; j < Cfg::kBJ; ++j) {

@@ -171,6 +171,12 @@ public:
     virtual Status enqueue_with_events(void* stream, void* const* events) = 0;
     // Launch j of the list alone (for timing one kernel back to back).
     virtual Status enqueue_launch(std::size_t j, void* stream = nullptr) = 0;
+    // `count` enqueues back to back on the same buffers. With graph_replay,
+    // runs of kGraphSteps steps replay one captured graph of that many
+    // steps (one submission per run instead of per step); the rest replay
+    // the one-step graph.
+    virtual Status enqueue_steps(int count, void* stream = nullptr) = 0;
+    static constexpr int kGraphSteps = 16;
     virtual Status synchronize() = 0;
     // Waits for the device, then copies the outputs to the host.
     virtual Status download_outputs(const std::vector<float*>& host_outputs) = 0;

@@ -127,7 +127,10 @@ MC_API int mc_enqueue_launch(void* handle, int j, void* stream);
  * at set_outputs[r * num_outputs ...], as mc_bind_inputs / mc_bind_outputs
  * take them; the last set used stays bound), then enqueues the whole step
  * (launch = -1) or only launch `launch` on `stream`. *host_us_per_step
- * (if not NULL) receives the host time per step of the loop. */
+ * (if not NULL) receives the host time per step of the loop. With sets = 0
+ * and launch = -1 under option graph_replay, runs of 16 steps replay one
+ * captured graph of 16 steps (one hipGraphLaunch per run), the rest the
+ * one-step graph. */
 MC_API int mc_enqueue_steps(void* handle, int launch, int steps, int sets, const void* const* set_inputs,
                             void* const* set_outputs, void* stream, double* host_us_per_step);
 /* The graph nodes each launch computes, launches separated by ';' and nodes

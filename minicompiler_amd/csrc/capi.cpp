@@ -439,7 +439,13 @@ MC_API int mc_enqueue_steps(void* h, int launch, int steps, int sets, const void
                        set_outputs + (static_cast<std::size_t>(r) + 1) * no);
     }
     const auto t0 = std::chrono::steady_clock::now();
-    for (int i = 0; i < steps; ++i) {
+    if (sets == 0 && launch < 0) {
+        // Every step on the same buffers: one call (graph_replay replays
+        // runs of captured steps).
+        Status st = c->exe->enqueue_steps(steps, stream);
+        if (!st.ok()) return fail("mc_enqueue_steps: " + st.message());
+    }
+    for (int i = 0; i < steps && (sets > 0 || launch >= 0); ++i) {
         if (sets > 0) {
             const std::size_t r = static_cast<std::size_t>(i % sets);
             Status st = c->exe->bind_inputs(ins[r]);

@@ -22,6 +22,27 @@ CASES = [("mlp_gelu", {"B": 256}, {}, 1e-4), ("mlp_gelu", {"B": 256}, {"matmul":
          ("gelu_chain", {"M": 64, "N": 4096}, {}, 1e-5), ("batchnorm_relu", {"R": 512, "C": 256}, {}, 1e-5)]
 
 
+@pytest.mark.parametrize("name,dims,opts,rtol", CASES[:3])
+def test_runs_of_captured_steps_equal_direct_launches(device, mc, oracle, name, dims, opts, rtol):
+    # enqueue_steps on one set of buffers under graph replay: 37 steps are
+    # two replays of a 16-step graph and five of the one-step graph. New
+    # inputs before each call; eager work between the calls.
+    print(f"case graph steps {name} {dims} {opts}", flush=True)
+    direct = mc.Compiled(path=mc.graph_path(name), dims=dims, options=opts)
+    replay = mc.Compiled(path=mc.graph_path(name), dims=dims, options={**opts, "graph": 1})
+    for rep, steps in enumerate((37, 16, 3)):
+        inputs = uniform_inputs(oracle, direct.input_sizes, 40 + rep)
+        want = direct.run(inputs)
+        replay.upload(inputs)
+        replay.enqueue_steps(steps)
+        got = replay.download()
+        for g, w in zip(got, want):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {rep} ({steps} steps)"
+    cpu = oracle.evaluate_compiled(direct, inputs)
+    for g, c in zip(got, cpu):
+        assert_close(g, c, rtol, rtol * max(1.0, max_abs(c)), "against the oracle")
+
+
 @pytest.mark.parametrize("name,dims,opts,rtol", CASES)
 def test_every_graph_replay_equals_direct_launches(device, mc, oracle, name, dims, opts, rtol):
     print(f"case graph {name} {dims} {opts}", flush=True)

@@ -1,0 +1,51 @@
+"""The FP32 ring planner (mchip_f32_ring_plan_cfg, host logic, no GPU): the
+tile configuration, grid and block it gives the bench's and the MLP's
+products on 256 CUs, and what a forced configuration gives. Configurations:
+1 wide (128x128, 4 waves), 2 mid, 3 big (256x256), 4 thin (32x128),
+6 wide8 (128x128, 8 waves)."""
+
+import ctypes
+
+import pytest
+
+NONE, WIDE, MID, BIG, THIN, WIDE8 = 0, 1, 2, 3, 4, 6
+
+
+@pytest.fixture(scope="module")
+def plan(mc):
+    f = mc.library().mchip_f32_ring_plan_cfg
+    f.argtypes = [ctypes.c_int] * 6 + [ctypes.POINTER(ctypes.c_uint)] * 2
+    f.restype = ctypes.c_int
+
+    def run(m, n, k, depth=1, cfg=NONE, cus=256):
+        grid, block = ctypes.c_uint(), ctypes.c_uint()
+        got = f(m, n, k, depth, cus, cfg, ctypes.byref(grid), ctypes.byref(block))
+        return got, grid.value, block.value
+
+    return run
+
+
+@pytest.mark.parametrize("m,n,k,depth,want", [
+    (8192, 8192, 8192, 1, (BIG, 256, 256)),      # 1024 tiles of 256x256, persistent
+    (4096, 4096, 4096, 1, (BIG, 256, 256)),
+    (8192, 2048, 512, 1, (BIG, 256, 256)),       # the MLP's GEMM1 at B=8192
+    (8192, 512, 2048, 1, (WIDE8, 256, 512)),     # its GEMM2: one 128x128 tile per CU
+    (2048, 2048, 2048, 1, (WIDE8, 256, 512)),
+    (1024, 1024, 1024, 4, (WIDE8, 256, 512)),    # 64 tiles x 4 splits
+    (16, 4096, 4096, 8, (THIN, 256, 256)),       # M <= 32
+])
+def test_the_planner_for_the_bench_and_mlp_shapes(plan, m, n, k, depth, want):
+    assert plan(m, n, k, depth) == want
+
+
+def test_a_forced_configuration_keeps_its_tiles_in_persistent_blocks(plan):
+    assert plan(8192, 512, 2048, cfg=WIDE) == (WIDE, 256, 256)      # 256 tiles, up to two blocks per CU
+    assert plan(4096, 4096, 4096, cfg=WIDE) == (WIDE, 512, 256)     # 1024 tiles
+    assert plan(8192, 512, 2048, cfg=BIG) == (BIG, 64, 256)         # 64 tiles of 256x256
+    assert plan(1000, 1024, 512, cfg=MID) == (MID, 128, 256)        # 16 x 8 tiles of 64x128
+    assert plan(1000, 1024, 512, cfg=WIDE8) == (WIDE8, 64, 512)
+
+
+def test_shapes_the_ring_cannot_take(plan):
+    assert plan(64, 64, 40)[0] == NONE   # K not a multiple of 32
+    assert plan(64, 66, 64)[0] == NONE   # N not a multiple of 4

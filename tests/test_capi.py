@@ -61,6 +61,8 @@ def test_no_device_calls_fail_cleanly_on_the_cpu(mc):
     if mc.device_count() > 0:
         pytest.skip("a device is present")
     assert mc.library().mc_gpu_device_json(None, 0, None, 0) == 1
+    assert mc.gpu_clock_sample() == (0.0, 0)  # mc_gpu_clock_sample returns 1 and zeroes both outputs
+    assert mc.gpu_clock_mhz() == 0.0
     with pytest.raises(mc.MinicompilerError, match="no HIP device|no usable HIP device"):
         mc.Compiled("input x : f32[4]\ny = neg x\noutput y\n", backend="hip")
     c = mc.Compiled("input x : f32[4]\ny = neg x\noutput y\n", backend="none")

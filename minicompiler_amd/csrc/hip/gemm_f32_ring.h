@@ -323,6 +323,11 @@ __device__ __forceinline__ void mc_ring_barrier() {
 // against 140.8-141.1. Big keeps each row's store right after its epilogue
 // (its 4 columns per lane already load a bias once): batched, its GEMM with
 // bias + GELU took 136.5-136.7 us against 135.3 (one MI355X, 3 runs each).
+// C goes out with non-temporal stores (every CU stores its tiles at about
+// the same moment at the end of a one-tile-per-CU launch): same bits, the
+// MLP's GEMM2 with b2 + residual 138.4-138.6 us against 139.4-139.6 and
+// 2048^3 131.0 against 132.1 us on one MI355X; the MLP's step and the other
+// sweep rows within 0.2%.
 // kSplit: raw partial sums that this launch adds, stored float by float
 // with device-scope stores (mc_split_store).
 template <class Cfg, bool kCheck, typename Epilogue, bool kSplit = false>
@@ -357,7 +362,7 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
                     const float x = acc[i][j][v];
                     BV::set(o, j, raw ? x : epilogue(x, static_cast<unsigned>(at + j)));
                 }
-                *reinterpret_cast<typename BV::type*>(out + at) = o;
+                __builtin_nontemporal_store(o, reinterpret_cast<typename BV::type*>(out + at));
             }
         return;
     }
@@ -390,7 +395,7 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
             for (int v = 0; v < 16; ++v) {
                 const int row = row_of(i0 + di, v);
                 if (kCheck && row >= m) continue;
-                *reinterpret_cast<typename BV::type*>(out + static_cast<long long>(row) * n + col) = o[di][v];
+                __builtin_nontemporal_store(o[di][v], reinterpret_cast<typename BV::type*>(out + static_cast<long long>(row) * n + col));
             }
     }
 }

@@ -25,7 +25,9 @@ chip. The other configurations time at least MIN_TIMED_MS of GPU work per
 timed loop (more steps than K when K would run less; `timed_steps` and
 `timed_launches` give the counts); the headline times exactly K steps.
 
-Prints ONE JSON line. `value` is the step's GEMM throughput (TFLOP/s = the
+Prints ONE JSON line on stdout (below SUMMARY_MAX_BYTES: headline fields,
+roofline, cpu_baseline and a short entry per config) and writes the full
+record, with every config's detail, to --out. `value` is the step's GEMM throughput (TFLOP/s = the
 two GEMMs' 2MNK FLOPs per step / ms_per_step). `roofline` is for the
 kernel that takes the most time; `kernels` lists every launch with its
 algorithmic work, achieved rate and fraction of the MI355X peak (HBM 8 TB/s;
@@ -344,6 +346,70 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
             "host_us_per_step": t["host_us_per_step"], "gbs": k["gbs"], "frac": k["frac"]}
 
 
+def bench_fusion(mc, dims: dict, rounds: int = 40) -> dict:
+    """The reference's fusion comparison (bench/bench_cuda.cpp:182-288): the
+    GELU chain compiled unfused (passes dne,fold,dne: one launch per op) and
+    fused (the default pipeline: one launch), both over buffer sets past the
+    MALL, timed in interleaved rounds whose variant order is a fresh seeded
+    shuffle each round. A sample is one pair of HIP events around a run of
+    steps on the executable's stream (enough steps for about 2 ms of work).
+    Time = median over rounds; speed-up = median over rounds of
+    unfused/fused in the same round; GB/s = the bytes every launch of the
+    variant reads and writes (the reference's bytes_moved) / median time.
+    The two variants' outputs must agree first (normwise, within 1e-5)."""
+    import random
+
+    x = mc.uniform(int(np.prod(list(dims.values()))), 1, -3.0, 3.0)
+    variants = []
+    for name, passes in (("unfused", "dne,fold,dne"), ("fused", "default")):
+        c = mc.Compiled(path=mc.graph_path("gelu_chain"), dims=dims, passes=passes)
+        rot, bufs = graph_rotation(mc, c, lambda: [x])
+        work = node_work(c.graph(), c.launch_nodes)
+        variants.append({"name": name, "passes": passes, "c": c, "rot": rot, "bufs": bufs,
+                         "bytes": sum(w["bytes"] for w in work), "samples": []})
+    outs = []
+    for v in variants:
+        v["c"].upload([x])
+        v["c"].enqueue()
+        outs.append(v["c"].download()[0].astype(np.float64))
+    diff = float(np.max(np.abs(outs[0] - outs[1])) / max(1.0, float(np.max(np.abs(outs[1])))))
+    if not diff <= 1e-5:
+        raise RuntimeError(f"fused and unfused GELU differ by {diff:g} (normwise)")
+    start, stop = mc.Event(), mc.Event()
+    for v in variants:
+        c = v["c"]
+        c.enqueue_steps(10, sets=v["rot"])
+        start.record(c.stream)
+        c.enqueue_steps(10, sets=v["rot"])
+        stop.record(c.stream)
+        c.synchronize()
+        v["steps"] = max(4, int(math.ceil(2.0 / max(start.elapsed_ms(stop) / 10, 1e-4))))
+        warm_up_for(WARM_SECONDS, lambda c=c, v=v: (c.enqueue_steps(v["steps"], sets=v["rot"]), c.synchronize()))
+    order = random.Random(20261005)
+    for _ in range(rounds):
+        for j in order.sample(range(len(variants)), len(variants)):
+            v = variants[j]
+            c = v["c"]
+            start.record(c.stream)
+            c.enqueue_steps(v["steps"], sets=v["rot"])
+            stop.record(c.stream)
+            c.synchronize()
+            v["samples"].append(start.elapsed_ms(stop) / v["steps"])
+    paired = sorted(u / f for u, f in zip(variants[0]["samples"], variants[1]["samples"]))
+    pct = lambda xs, q: xs[min(len(xs) - 1, int(q * len(xs)))]
+    out = {"config": "gelu_chain", "dims": dims, "rounds": rounds, "max_normwise_diff": diff,
+           "speedup": {"median": statistics.median(paired), "p10": pct(paired, 0.1), "p90": pct(paired, 0.9)}}
+    for v in variants:
+        ms = statistics.median(v["samples"])
+        out[v["name"]] = {"passes": v["passes"], "launches": v["c"].kernel_launches, "bytes_moved": v["bytes"],
+                          "ms": ms, "ms_range": [min(v["samples"]), max(v["samples"])],
+                          "steps_per_sample": v["steps"], "buffer_sets": len(v["rot"]),
+                          "gbs": v["bytes"] / (ms * 1e-3) / 1e9, "frac": v["bytes"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+        v["c"].close()
+        del v["bufs"]
+    return out
+
+
 def time_gemm(mc, launches, steps: int, warmup: int, min_ms: float | None = None) -> dict:
     """Mean duration of one launch, over `steps` back-to-back launches that
     cycle through `launches` (one closure per operand set, each enqueueing
@@ -497,10 +563,10 @@ def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
     gelu_tanh(x w + bias), fp32 in and out) compiled with the bf16 / fp16
     matrix-core kernel. A step is one launch: it rounds x to 16 bits (w was
     rounded once, at compile time), then runs the GEMM with bias+GELU fused
-    into its store. The rounding of x alone (the same conversion on a copy
-    of x, timed the same way) is reported as `round_x_ms`;
-    `gemm_epilogue_ms` = the launch less the rounding, and
-    `gemm_epilogue_tflops` counts the GEMM's 2MNK FLOPs over it."""
+    into its store. `tflops` counts the GEMM's 2MNK FLOPs over the measured
+    step (rounding of x included). The rounding of x alone (the same
+    conversion on a copy of x, timed the same way) is reported beside it as
+    `round_x_ms`, a separate measurement; nothing is subtracted."""
     out = []
     for m, n, k in shapes:
         x = mc.uniform(m * k, 1, -1.0, 1.0)
@@ -518,13 +584,12 @@ def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
             rounds = [lambda st, a=a, h=h: mc.convert_f32(dtype, a.ptr, h.ptr, m * k, st) for a, h in xs]
             round_ms = time_gemm(mc, rounds, steps, warmup)["graph"]["ms"]
             del xs, rounds
-            gemm_ms = launch_ms - round_ms
-            tf = 2.0 * m * n * k / (gemm_ms * 1e-3) / 1e12
+            tf = 2.0 * m * n * k / (t["ms_per_step"] * 1e-3) / 1e12
             out.append({"m": m, "n": n, "k": k, "kernel": kernel, "launches": names, "buffer_sets": len(rot),
                         "ms_per_step": t["ms_per_step"], "launch_ms": launch_ms, "round_x_ms": round_ms,
-                        "gemm_epilogue_ms": gemm_ms, "gemm_epilogue_tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
-            log(f"{kernel} {m}x{n}x{k} + bias + gelu: step {t['ms_per_step']:.3f} ms (rounding x {round_ms:.3f} ms), "
-                f"fused GEMM {gemm_ms:.3f} ms {tf:.1f} TFLOP/s")
+                        "tflops": tf, "frac": tf / PEAK_BF16_TFLOPS})
+            log(f"{kernel} {m}x{n}x{k} + bias + gelu: step {t['ms_per_step']:.3f} ms {tf:.1f} TFLOP/s "
+                f"(its GEMM launch {launch_ms:.3f} ms; rounding x alone {round_ms:.3f} ms)")
     return out
 
 
@@ -695,6 +760,13 @@ def cpu_baselines(mc, args, cpu_s: float, headline_s: float) -> dict:
             out[("epilogue", m, n, k)] = cpu_baseline_graph(
                 mc, "matmul_bias_gelu", lambda r, k=k, n=n: {"M": r, "K": k, "N": n}, m, k,
                 lambda cnt: mc.uniform(cnt, 1, -1.0, 1.0), 2.0 * n * k, "TFLOP/s", 2, cpu_s)
+    if args.workload == "mlp" and not args.quick:
+        # The batch sweep's small batches: the whole batch each (rows of the
+        # MLP are independent, but each row reports its own measured batch).
+        for b in (256, 1024):
+            out[f"mlp_b{b}"] = cpu_baseline_graph(mc, "mlp_gelu", lambda r: {"B": r}, b, 512,
+                                                  lambda cnt: mc.uniform(cnt, 1, -1.0, 1.0), 4.0 * 512 * 2048,
+                                                  "TFLOP/s", min(b, 64), cpu_s)
     if args.workload == "mlp" and headline_s > 0:
         out["headline"] = cpu_baseline(256, headline_s)
     return out
@@ -711,6 +783,11 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
             e["cpu_baseline"] = cpu["gelu"]
         cfgs["gelu_4096x4096"] = e
         log(f"gelu: {e['gbs']:.0f} GB/s, host {e['host_us_per_step']:.1f} us/step")
+        f = bench_fusion(mc, {"M": 4096, "N": 4096})
+        cfgs["gelu_fusion_4096x4096"] = f
+        log(f"gelu fusion: unfused {f['unfused']['launches']} launches {f['unfused']['ms'] * 1e3:.1f} us "
+            f"({f['unfused']['gbs']:.0f} GB/s), fused {f['fused']['launches']} launch {f['fused']['ms'] * 1e3:.1f} us "
+            f"({f['fused']['gbs']:.0f} GB/s), speed-up {f['speedup']['median']:.2f}x")
     if want("batchnorm"):
         e = bench_elementwise_graph(mc, "batchnorm_relu", {"R": 200704, "C": 256},
                                     lambda n: mc.normal(n, 1, 0.0, 1.0), args.steps, args.warmup)
@@ -733,8 +810,8 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
                                "host_us_per_step": r["timing"]["host_us_per_step"],
                                "launch_ms": r["timing"]["launch_ms"]}
                 del r
-            if "headline" in cpu:
-                entry["cpu_baseline"] = cpu["headline"]
+            if f"mlp_b{b}" in cpu:
+                entry["cpu_baseline"] = cpu[f"mlp_b{b}"]
             cfgs[f"mlp_b{b}"] = entry
             log(f"mlp B={b}: direct {entry['direct']['ms_per_step'] * 1e3:.1f} us/step, "
                 f"graph replay {entry['graph_replay']['ms_per_step'] * 1e3:.1f} us/step, "
@@ -761,6 +838,103 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
         cfgs["gemm_bf16_fp16_bias_gelu"] = ep
 
 
+# The final stdout line stays below this many bytes (the record a harness
+# parses may be only the tail of stdout); everything else goes to --out.
+SUMMARY_MAX_BYTES = 6000
+
+
+def _r(x, nd=4):
+    """A float rounded for the summary line (None stays None)."""
+    return None if x is None else float(f"{x:.{nd}g}")
+
+
+def _cpu_short(e: dict | None) -> dict | None:
+    if not e:
+        return None
+    out = {"value": _r(e["value"]), "threads": e.get("threads", 1)}
+    if "all_cores" in e:
+        out["all_cores"] = _r(e["all_cores"]["value"])
+        out["all_threads"] = e["all_cores"]["threads"]
+    return out
+
+
+def summary_configs(cfgs: dict) -> dict:
+    """Per config: value, unit and roofline fraction, with the CPU
+    baseline's one-thread and all-thread values; detail stays in --out."""
+    out = {}
+    for name in ("gelu_4096x4096", "batchnorm_relu_200704x256"):
+        if name in cfgs:
+            e = cfgs[name]
+            out[name] = {"value": _r(e["gbs"]), "unit": "GB/s", "frac": _r(e["frac"], 3),
+                         "cpu": _cpu_short(e.get("cpu_baseline"))}
+    if "gelu_fusion_4096x4096" in cfgs:
+        f = cfgs["gelu_fusion_4096x4096"]
+        out["gelu_fusion_4096x4096"] = {
+            "speedup": _r(f["speedup"]["median"]),
+            **{v: {"launches": f[v]["launches"], "ms": _r(f[v]["ms"]), "gbs": _r(f[v]["gbs"])}
+               for v in ("unfused", "fused")}}
+    for b in (256, 1024):
+        if f"mlp_b{b}" in cfgs:
+            e = cfgs[f"mlp_b{b}"]
+            out[f"mlp_b{b}"] = {**{m: {"us": _r(e[m]["ms_per_step"] * 1e3), "value": _r(e[m]["tflops"])}
+                                   for m in ("direct", "graph_replay", "autotuned")},
+                                "unit": "TFLOP/s", "cpu": _cpu_short(e.get("cpu_baseline"))}
+    if "gemm_fp32" in cfgs:
+        rows = {}
+        for e in cfgs["gemm_fp32"]:
+            r = {"value": _r(e["tflops"]), "frac": _r(e["frac"], 3), "graph": _r(e["graph"]["tflops"]),
+                 "cpu": _r(e["cpu_baseline"]["value"]) if "cpu_baseline" in e else None}
+            if "gbs" in e:
+                r.update({"gbs": _r(e["gbs"]), "frac_hbm": _r(e["frac_hbm"], 3), "graph_gbs": _r(e["graph"]["gbs"])})
+            rows[f"{e['m']}x{e['n']}x{e['k']}"] = r
+        out["gemm_fp32"] = {"unit": "TFLOP/s", "rows": rows}
+    for key in ("gemm_bf16_fp16", "gemm_bf16_fp16_bias_gelu"):
+        if key in cfgs:
+            out[key] = {"unit": "TFLOP/s",
+                        "rows": {f"{e['kernel'][12:]} {e['m']}x{e['n']}x{e['k']}":
+                                 {"value": _r(e["tflops"]), "frac": _r(e["frac"], 3),
+                                  "cpu": _r(e["cpu_baseline"]["value"]) if "cpu_baseline" in e else None}
+                                 for e in cfgs[key]}}
+    return out
+
+
+def summary_line(full: dict) -> dict:
+    """The one JSON line printed on stdout: the headline fields, `roofline`
+    (with `traffic`), `cpu_baseline` (short sample), each launch of the
+    headline step and one short entry per other config. Guaranteed below
+    SUMMARY_MAX_BYTES: optional parts are dropped, largest first, if not."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+            "vs_baseline", "dtype", "data", "config", "roofline")
+    line = {k: full[k] for k in keep if k in full}
+    if "config" in line:
+        line["config"] = {k: v for k, v in line["config"].items() if k != "order"}
+    if "cpu_baseline" in full:
+        c = full["cpu_baseline"]
+        line["cpu_baseline"] = {"value": c["value"], "unit": c["unit"], "cores": c["cores"], "kind": c["kind"],
+                                "sample": c["sample"][:240]}
+        if "all_cores" in c:
+            line["cpu_baseline"]["all_cores"] = {"value": c["all_cores"]["value"],
+                                                 "threads": c["all_cores"]["threads"]}
+    if "kernels" in full:
+        line["kernels"] = [{"launch": k["launch"][:60], "ms": _r(k["ms"]),
+                            ("tflops" if k["bound"] == "mfma" else "gbs"): _r(k.get("tflops", k.get("gbs"))),
+                            "frac": _r(k["frac"], 3)} for k in full["kernels"]]
+    if "device" in full:
+        d = full["device"]
+        line["device"] = {"name": d.get("name"), "cu_count": d.get("cu_count"),
+                          "clock_median_mhz": d.get("clocks", {}).get("median_mhz"),
+                          "clock_timed_steps_median_mhz": d.get("clocks_timed_steps", {}).get("median_mhz")}
+    if full.get("configs"):
+        line["configs"] = summary_configs(full["configs"])
+    if full.get("full_record"):
+        line["full_record"] = full["full_record"]
+    for drop in ("configs", "kernels", "device"):
+        if len(json.dumps(line)) < SUMMARY_MAX_BYTES:
+            break
+        line.pop(drop, None)
+    return line
+
+
 def main() -> int:
     global MIN_TIMED_MS
     ap = argparse.ArgumentParser()
@@ -778,6 +952,8 @@ def main() -> int:
     ap.add_argument("--config-cpu-seconds", type=float, default=1.5, help="each other config's CPU baseline")
     ap.add_argument("--min-timed-ms", type=float, default=MIN_TIMED_MS,
                     help="GPU work per timed loop of the other configs (0 under rocprofv3)")
+    ap.add_argument("--out", default=str(ROOT / "results" / "bench_full.json"),
+                    help="file for the full record (every config's detail); '' for none")
     args = ap.parse_args()
     MIN_TIMED_MS = args.min_timed_ms
 
@@ -875,7 +1051,13 @@ def main() -> int:
                                         "period_ms": 50}
     if "headline" in cpu:
         line["cpu_baseline"] = cpu["headline"]
-    print(json.dumps(line), flush=True)
+    if args.out:
+        out = Path(args.out)
+        out.parent.mkdir(parents=True, exist_ok=True)
+        out.write_text(json.dumps(line, indent=1) + "\n")
+        line["full_record"] = str(out)
+        log(f"full record: {out} ({out.stat().st_size} bytes)")
+    print(json.dumps(summary_line(line)), flush=True)
     return 0
 
 

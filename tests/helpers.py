@@ -65,3 +65,29 @@ def uniform_inputs(oracle, sizes, seed: int, lo: float = -1.0, hi: float = 1.0) 
     """Input k = uniform(n_k, seed + k, lo, hi), as make_random_inputs does
     (src/runtime/host_tensor.cpp:7-14)."""
     return [oracle.uniform(int(n), seed + k, lo, hi) for k, n in enumerate(sizes)]
+
+
+def run_into_prefilled(mc, compiled, inputs) -> list[np.ndarray]:
+    """Runs `compiled` on `inputs` with every output bound to a device
+    buffer whose bytes are all 0xFF (a NaN in every float), so an element the
+    kernels never write reads back as NaN (the reference's NaN prefill,
+    tests/test_cuda_backend.cpp:297). Returns the outputs as float32 arrays."""
+    bufs = [mc.DeviceBuffer(4 * n) for n in compiled.output_sizes]
+    for b in bufs:
+        b.fill_bytes(0xFF)
+    compiled.bind_outputs([b.ptr for b in bufs])
+    compiled.upload(inputs)
+    compiled.enqueue()
+    compiled.synchronize()
+    outs = [b.download() for b in bufs]
+    compiled.bind_outputs([None] * len(bufs))
+    return outs
+
+
+def row_blocks(total: int, rows: int, seed: int, middle: int = 2) -> list[int]:
+    """First rows of the blocks a full-size check compares: the first and the
+    last `rows` rows, plus `middle` seeded starts in between (not aligned to
+    a tile, so each straddles a tile boundary)."""
+    rng = np.random.default_rng(seed)
+    mids = sorted(int(s) for s in rng.integers(rows, total - 2 * rows, middle))
+    return [0] + mids + [total - rows]

@@ -15,16 +15,19 @@ gelu_tanh, whose derivative peaks at 1.1289 near x = 1.5):
   group's rtol 1e-5), which isolates accumulation and epilogue from input
   rounding.
 Rows of a product are independent, so the epilogue graph is checked on its
-first and last 256 rows (the first and the last tile row) against the
+first and last 256 rows (the first and the last tile row) and on two seeded
+256-row blocks in between (each straddling a tile boundary) against the
 oracle run on those rows alone; the bare GEMM on 2000 sampled elements
-(bench/bench_cuda.cpp:386-413). Every output is prefilled with NaN."""
+(bench/bench_cuda.cpp:386-413). Every output is prefilled with NaN on the
+device (the graph's output is bound to a 0xFF-filled buffer) and checked
+for unwritten elements everywhere."""
 
 import os
 
 import numpy as np
 import pytest
 
-from helpers import U32, gamma, lowp_gemm_bound
+from helpers import U32, gamma, lowp_gemm_bound, row_blocks, run_into_prefilled
 
 pytestmark = pytest.mark.gpu
 
@@ -85,7 +88,7 @@ EPILOGUE_SHAPES = [(8192, 8192, 8192), (4096, 4096, 14336)]
 
 @pytest.mark.parametrize("kernel,dtype,u,subnormals", FORMATS)
 @pytest.mark.parametrize("m,k,n", EPILOGUE_SHAPES)
-def test_gemm_with_fused_bias_gelu_matches_the_oracle_on_first_and_last_rows(device, mc, threaded_oracle, kernel,
+def test_gemm_with_fused_bias_gelu_matches_the_oracle_on_row_blocks(device, mc, threaded_oracle, kernel,
                                                                               dtype, u, subnormals, m, k, n):
     oracle = threaded_oracle
     rows = 256
@@ -96,8 +99,9 @@ def test_gemm_with_fused_bias_gelu_matches_the_oracle_on_first_and_last_rows(dev
     assert c.kernel_launches <= 2, "the bias + GELU group is fused into the GEMM's store"
     assert any(len(ids) > 1 for ids in c.launch_nodes)
     x = oracle.uniform(m * k, 1, -1.0, 1.0)
-    gpu = c.run([x])[0].reshape(m, n)
-    assert not np.any(np.isnan(gpu)), "an element of y was not written"
+    gpu = run_into_prefilled(mc, c, [x])[0]
+    assert not np.any(np.isnan(gpu)), f"{np.count_nonzero(np.isnan(gpu))} elements of y were not written"
+    gpu = gpu.reshape(m, n)
     del c
     # The same graph on `rows` rows, passes only: its constants are seeded per
     # tensor, so w and bias equal the full graph's.
@@ -110,7 +114,7 @@ def test_gemm_with_fused_bias_gelu_matches_the_oracle_on_first_and_last_rows(dev
     rnd = oracle.round_bf16 if dtype == 1 else oracle.round_f16
     wr = rnd(w)
     xs = x.reshape(m, k)
-    for first in (0, m - rows):
+    for first in row_blocks(m, rows, seed=m + n):
         print(f"  rows {first}..{first + rows - 1}", flush=True)
         got = gpu[first:first + rows].reshape(-1).astype(np.float64)
         xa = np.ascontiguousarray(xs[first:first + rows]).reshape(-1)

@@ -5,9 +5,12 @@
   scale (tests/test_cuda_backend.cpp:412-414).
 - The MLP block at B=8192 (GEMM1 with bias + GELU fused into its store, GEMM2
   with b2 + residual): the rows of a batch are independent, so the oracle's
-  output for B=256 rows of x is the B=8192 output of those rows. The first
-  and the last 256 rows (the last tile row of both GEMMs) are checked at the
-  FP32 graph tolerance, rtol 1e-4 plus 1e-4 of the scale.
+  output for B=256 rows of x is the B=8192 output of those rows. The output
+  is bound to a device buffer prefilled with NaN and checked for unwritten
+  elements everywhere; the first and the last 256 rows (the last tile row of
+  both GEMMs) and two seeded blocks in between, each straddling a tile
+  boundary, are checked at the FP32 graph tolerance, rtol 1e-4 plus 1e-4 of
+  the scale.
 - The FP32 GEMM sweep (config 4) with the kernel and split count that auto
   resolves to on this device, as launch_matmul runs them: 2000 sampled
   elements per shape (all elements for the two small outputs) against
@@ -18,7 +21,7 @@
 import numpy as np
 import pytest
 
-from helpers import assert_close, fp32_gemm_bound, max_abs
+from helpers import assert_close, fp32_gemm_bound, max_abs, row_blocks, run_into_prefilled
 
 pytestmark = pytest.mark.gpu
 
@@ -28,7 +31,7 @@ def test_gelu_4096_squared_matches_the_oracle_everywhere(device, mc, oracle):
     c = mc.Compiled(path=mc.graph_path("gelu_chain"), dims={"M": 4096, "N": 4096})
     assert c.kernel_launches == 1
     x = oracle.uniform(4096 * 4096, 1, -3.0, 3.0)
-    gpu = c.run([x])[0]
+    gpu = run_into_prefilled(mc, c, [x])[0]
     cpu = oracle.evaluate_compiled(c, [x])[0]
     assert_close(gpu, cpu, 1e-5, 1e-5 * max(1.0, max_abs(cpu)), "gelu 4096^2")
 
@@ -38,24 +41,26 @@ def test_batchnorm_relu_at_200704_rows_matches_the_oracle_everywhere(device, mc,
     c = mc.Compiled(path=mc.graph_path("batchnorm_relu"), dims={"R": 200704, "C": 256})
     assert c.kernel_launches == 1
     x = oracle.normal(200704 * 256, 1, 0.0, 1.0)
-    gpu = c.run([x])[0]
+    gpu = run_into_prefilled(mc, c, [x])[0]
     cpu = oracle.evaluate_compiled(c, [x])[0]
     assert_close(gpu, cpu, 1e-5, 1e-5 * max(1.0, max_abs(cpu)), "batchnorm 200704x256")
     assert np.all(gpu >= 0.0), "relu output below zero"
 
 
-def test_mlp_at_batch_8192_matches_the_oracle_on_its_first_and_last_rows(device, mc, oracle):
+def test_mlp_at_batch_8192_matches_the_oracle_on_row_blocks_after_a_nan_prefill(device, mc, oracle):
     print("case full mlp_gelu B=8192", flush=True)
     batch, d, rows = 8192, 512, 256
     c = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": batch})
     assert c.kernel_launches == 2, "both GEMMs carry their groups"
     x = oracle.uniform(batch * d, 1, -1.0, 1.0)
-    gpu = c.run([x])[0].reshape(batch, d)
+    gpu = run_into_prefilled(mc, c, [x])[0]
+    assert not np.any(np.isnan(gpu)), f"{np.count_nonzero(np.isnan(gpu))} elements of y were not written"
+    gpu = gpu.reshape(batch, d)
     # The same graph at B=256: its constants are seeded per tensor, so they
     # equal the B=8192 graph's.
     part = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": rows}, backend="none")
     xs = x.reshape(batch, d)
-    for first in (0, batch - rows):
+    for first in row_blocks(batch, rows, seed=batch):
         cpu = oracle.evaluate_compiled(part, [np.ascontiguousarray(xs[first:first + rows]).reshape(-1)])[0]
         got = gpu[first:first + rows].reshape(-1)
         assert_close(got, cpu, 1e-4, 1e-4 * max(1.0, max_abs(cpu)), f"mlp rows {first}..{first + rows - 1}")

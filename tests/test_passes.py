@@ -258,9 +258,9 @@ def test_parser_errors_and_printer(mc):
         "input x : f32[0]\noutput x\n": "invalid shape",
         "input x : f32[2]\ninput x : f32[2]\noutput x\n": "defined twice",
         "input x : f32[2]\n": "no outputs",
-        "dim B = 4\ndim B = 5\ninput x : f32[B]\noutput x\n": "declared twice",
+        "dim B = 4\ndim B = 5\ninput x : f32[B]\noutput x\n": "already declared",
         "input x : f32[65536, 65536]\noutput x\n": "2^31 - 1",
-        "const c : f32[2] = uniform(seed=1, lo=2, hi=1)\noutput c\n": "lo < hi",
+        "const c : f32[2] = uniform(seed=1, lo=2, hi=1)\noutput c\n": "lo must be below hi",
         "input x : f32[2, 3]\ninput y : f32[4]\nz = add x, y\noutput z\n": "cannot broadcast",
     }
     for text, needle in bad.items():
@@ -291,3 +291,129 @@ def test_uniform_constants_carry_the_reference_golden_bits(mc):
 def test_normal_constants_match_the_oracle_generator(mc, oracle):
     c = compile_none(mc, "const v : f32[1001] = normal(seed=7, mean=0.5, std=0.1)\noutput v\n", passes="none")
     assert np.array_equal(c.constant(0), oracle.normal(1001, 7, 0.5, 0.1))
+
+
+# The reference's parser known answers, message for message
+# (tests/test_parser.cpp:66-123).
+REFERENCE_PARSE_ERRORS = [
+    ("input x : f32[4]\ny = frobnicate x\noutput y", "line 2: unknown op 'frobnicate'"),
+    ("input x : f32[4]\ny = relu z\noutput y", "line 2: unknown value 'z'"),
+    ("input x : f32[4]\nx = relu x\noutput x", "line 2: 'x' is defined twice"),
+    ("input x : i32[4]\noutput x", "line 1: unsupported element type 'i32' (only f32)"),
+    ("input x : f32[N]\noutput x", "line 1: unknown dim 'N'"),
+    ("const c : f32[3] = [1, 2]\noutput c", "line 1: expected 3 values for f32[3], got 2"),
+    ("input x : f32[4]\n", "the graph declares no outputs"),
+    ("input x : f32[4] ;", "line 1: unexpected character ';'"),
+    ("input x : f32[4]\ny = relu x x", "line 2: unexpected 'x'"),
+    ("const c : f32[-1] = 0\noutput c",
+     "line 1: invalid shape [-1]: dimensions must be >= 1 and the total at most 2^31 - 1 elements"),
+]
+REFERENCE_INVALID_SHAPES = ["const c : f32[-1] = uniform(seed=1, lo=0, hi=1)\noutput c",
+                            "input x : f32[7, 7905747460161236407]\noutput x",
+                            "const c : f32[4294967296, 4294967296] = 1\noutput c",
+                            "input x : f32[4, 0]\noutput x"]
+REFERENCE_EXAMPLE = """
+# A small MLP layer.
+graph layer
+dim B = 2
+input x : f32[B, 3]
+const w : f32[3, 4] = uniform(seed=7, lo=-0.5, hi=0.5)
+const b : f32[4] = [1, 2, 3, 4]
+const half : f32[] = 0.5
+h = matmul x, w
+hb = add h, b      # bias broadcast over rows
+y = mul hb, half
+output y, h
+"""
+
+
+def parse_error(mc, text, dims=None):
+    try:
+        compile_none(mc, text, passes="none", dims=dims)
+    except mc.MinicompilerError as e:
+        return str(e)
+    return "<parsed>"
+
+
+@pytest.mark.parametrize("text,message", REFERENCE_PARSE_ERRORS)
+def test_parser_reports_the_reference_messages(mc, text, message):
+    assert parse_error(mc, text) == message
+
+
+def test_parser_rejects_invalid_shapes_before_allocating(mc):
+    for text in REFERENCE_INVALID_SHAPES:
+        assert parse_error(mc, text).startswith("line 1: invalid shape"), text
+
+
+def test_parser_carries_ir_shape_errors_with_the_value_name(mc):
+    err = parse_error(mc, "input a : f32[4, 8]\ninput b : f32[4]\nc = add a, b\noutput c")
+    assert err.startswith("line 3: c: add: cannot broadcast"), err
+
+
+def test_parser_reads_every_statement_kind_of_the_reference_example(mc, oracle):
+    c = compile_none(mc, REFERENCE_EXAMPLE, passes="none")
+    g = c.graph()
+    assert g["name"] == "layer" and len(g["nodes"]) == 7 and c.num_inputs == 1 and c.num_outputs == 2
+    assert node_named(g, "x")["shape"] == [2, 3] and node_named(g, "y")["shape"] == [2, 4]
+    assert c.constant(node_named(g, "b")["id"]).tolist() == [1, 2, 3, 4]
+    assert c.constant(node_named(g, "half")["id"]).tolist() == [0.5]
+    assert np.array_equal(c.constant(node_named(g, "w")["id"]), oracle.uniform(12, 7, -0.5, 0.5))
+    wide = compile_none(mc, REFERENCE_EXAMPLE, passes="none", dims={"B": 64})
+    assert node_named(wide.graph(), "y")["shape"] == [64, 4]
+    assert "no dim 'Q'" in parse_error(mc, REFERENCE_EXAMPLE, dims={"B": 64, "Q": 1})
+    p = c.print_graph()
+    assert "graph layer\n" in p
+    assert "%0 x = input : f32[2,3]" in p
+    assert "%2 b = const [1, 2, 3, 4] : f32[4]" in p
+    assert "%6 y = mul %5, %3 : f32[2,4]  (output)" in p
+
+
+def test_parser_keeps_large_seeds_exact(mc, oracle):
+    a = compile_none(mc, "const c : f32[8] = uniform(seed=9007199254740992, lo=0, hi=1)\noutput c", passes="none")
+    b = compile_none(mc, "const c : f32[8] = uniform(seed=9007199254740993, lo=0, hi=1)\noutput c", passes="none")
+    assert not np.array_equal(a.constant(0), b.constant(0))
+    assert np.array_equal(b.constant(0), oracle.uniform(8, 9007199254740993, 0.0, 1.0))
+
+
+def test_parser_ignores_comments_blank_lines_and_carriage_returns(mc):
+    c = compile_none(mc, "# header\r\n\r\ninput x : f32[2]   # trailing\r\ny = exp x\r\noutput y\r\n", passes="none")
+    assert len(c.graph()["nodes"]) == 2
+
+
+def test_parser_accepts_scalars_and_signed_numbers(mc):
+    c = compile_none(mc, "const c : f32[] = -1.5e-1\nconst d : f32[2] = [-2, +.5]\ny = mul c, d\noutput y",
+                     passes="none")
+    g = c.graph()
+    assert c.constant(node_named(g, "c")["id"]).tolist() == [np.float32(-0.15)]
+    assert c.constant(node_named(g, "d")["id"]).tolist() == [-2.0, 0.5]
+
+
+@pytest.mark.parametrize("text,needle", [
+    ("const c : f32[2] = uniform(seed=1, lo=0)\noutput c", "missing 'hi'"),
+    ("const c : f32[2] = uniform(seed=1, lo=0, lo=1, hi=2)\noutput c", "'lo' twice"),
+    ("const c : f32[2] = uniform(seed=1, lo=0, mid=1, hi=2)\noutput c", "no argument 'mid'"),
+    ("const c : f32[2] = uniform(seed=-1, lo=0, hi=2)\noutput c", "seed '-1'"),
+    ("const c : f32[2] = normal(seed=1, mean=0, std=0)\noutput c", "std must be positive"),
+    ("const c : f32[2] = poisson(seed=1)\noutput c", "no initializer named 'poisson'"),
+    ("const c : f32[2] = 1e999\noutput c", "number '1e999'"),
+    ("dim B = 1.5\ninput x : f32[B]\noutput x", "'1.5' is not a 64-bit integer"),
+    ("dim B = 0\ninput x : f32[B]\noutput x", "not a positive size"),
+    ("input x : f32[2]\ngraph late\noutput x", "has to precede every node"),
+    ("input x : f32[2]\nfoo x\noutput x", "neither a statement keyword nor an assignment"),
+    ("input x : f32[2\noutput x", "expected ',' or ']' before the end of the line"),
+    ("input x f32[2]\noutput x", "expected ':' where 'f32' stands"),
+])
+def test_parser_names_what_is_wrong(mc, text, needle):
+    assert needle in parse_error(mc, text), parse_error(mc, text)
+
+
+def test_parser_terminates_on_random_text(mc):
+    """Every text over the language's alphabet parses or fails (a lexer that
+    stops advancing on some number form would hang here)."""
+    rng = np.random.default_rng(5)
+    pieces = ["input", "const", "dim", "output", "graph", "x", "y", "f32", ":", "=", ",", "[", "]", "(", ")",
+              "0.5", ".5", "1.", "5.5.5", "1e", "1e-", "2E+3", "+", "-", "+.", "-.e", "..", "#c", "\n", " ", "\r",
+              ";", "uniform", "seed=1", "relu", "add"]
+    for _ in range(3000):
+        text = "".join(rng.choice(pieces, size=int(rng.integers(1, 14))))
+        parse_error(mc, text)

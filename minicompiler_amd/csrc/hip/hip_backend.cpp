@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <map>
 #include <thread>
 
 namespace minicompiler::hip {
@@ -114,6 +115,14 @@ void split_layout(int k, int splits, int* k_split, int* depth) {
 }
 
 class HipExecutableImpl final : public HipExecutable {
+    // graph_replay: per binding of caller memory, the captured enqueue and a
+    // run of kGraphSteps captured enqueues.
+    struct Captured {
+        void* one = nullptr;
+        void* run = nullptr;
+    };
+    static constexpr std::size_t kMaxCapturedBindings = 64;
+
 public:
     HipExecutableImpl(const Graph& graph, const HipOptions& options)
         : graph_(graph), options_(options), plan_(plan_memory(graph_)) {}
@@ -297,8 +306,10 @@ public:
     Status enqueue(void* stream) override {
         if (!options_.graph_replay) return enqueue_with_events(stream, nullptr);
         void* s = stream ? stream : stream_;
-        if (graph_exec_ == nullptr) MCHIP_TRY_STATUS(capture_steps(s, 1, &graph_exec_));
-        MCHIP_TRY(mchip_graph_launch(graph_exec_, s));
+        Captured& cap = captured_for_binding();
+        if (cap.one == nullptr) MCHIP_TRY_STATUS(capture_steps(s, 1, &cap.one));
+        MCHIP_TRY(mchip_graph_launch(cap.one, s));
+        graphs_launched_ = true;
         return Status();
     }
 
@@ -311,8 +322,10 @@ public:
             // launches of a small graph's step (19-26 us on an MI355X against
             // 5.3 us), so single-step replays leave the GPU waiting; a run of
             // kGraphSteps steps pays it once.
-            if (graph_steps_exec_ == nullptr) MCHIP_TRY_STATUS(capture_steps(s, kGraphSteps, &graph_steps_exec_));
-            for (; done + kGraphSteps <= count; done += kGraphSteps) MCHIP_TRY(mchip_graph_launch(graph_steps_exec_, s));
+            Captured& cap = captured_for_binding();
+            if (cap.run == nullptr) MCHIP_TRY_STATUS(capture_steps(s, kGraphSteps, &cap.run));
+            for (; done + kGraphSteps <= count; done += kGraphSteps) MCHIP_TRY(mchip_graph_launch(cap.run, s));
+            graphs_launched_ = true;
         }
         for (; done < count; ++done) MCHIP_TRY_STATUS(enqueue(s));
         return Status();
@@ -385,7 +398,6 @@ public:
             bound_[static_cast<std::size_t>(graph_.inputs()[k])] = const_cast<void*>(device_inputs[k]);
         }
         refresh_pointers();
-        drop_graph();
         return Status();
     }
 
@@ -400,7 +412,6 @@ public:
             if (is_compute(graph_.node(id).op)) bound_[static_cast<std::size_t>(id)] = device_outputs[k];
         }
         refresh_pointers();
-        drop_graph();
         return Status();
     }
 
@@ -421,9 +432,19 @@ public:
         for (const Launch& l : launches_) {
             const Node& node = graph_.node(l.node);
             if (l.kind == Launch::Kind::Matmul || l.kind == Launch::Kind::FusedMatmul) {
+                // The K ranges that run (the split count is an upper bound
+                // for the narrow-tile body), and the count asked for when
+                // they differ.
+                const int ranges = l.kind == Launch::Kind::FusedMatmul || l.lowp
+                                       ? (l.lowp ? 1 : l.depth)
+                                       : mchip_matmul_k_ranges(static_cast<int>(l.matmul), l.m, l.n, l.k, l.splits,
+                                                               l.ring_cfg);
                 std::string name = std::string("matmul ") + matmul_kernel_name(l.matmul) + " " + std::to_string(l.m) +
-                                   "x" + std::to_string(l.n) + "x" + std::to_string(l.k) +
-                                   (l.splits > 1 ? " splits=" + std::to_string(l.splits) : "");
+                                   "x" + std::to_string(l.n) + "x" + std::to_string(l.k);
+                if (l.splits > 1 || ranges > 1) {
+                    name += " splits=" + std::to_string(ranges);
+                    if (ranges != l.splits) name += " of " + std::to_string(l.splits);
+                }
                 if (folds(l)) name += ", summed in the GEMM";
                 if (l.kind == Launch::Kind::FusedMatmul) {
                     const Node& f = graph_.node(l.epilogue_node);
@@ -516,11 +537,35 @@ private:
                mchip_split_k_folds(l.m, l.n, l.k, l.splits, l.ring_cfg) != 0;
     }
 
-    // The captured graph holds the kernel arguments of the time of capture.
+    // graph_replay: a captured graph holds the kernel arguments of the time
+    // of capture, so graphs are kept per binding of caller memory (bound
+    // inputs and outputs): a caller cycling through buffer sets replays one
+    // graph per set, and a rebinding never destroys a graph that may run.
+    std::vector<void*> binding_key() const {
+        std::vector<void*> key(bound_);
+        key.insert(key.end(), output_bound_.begin(), output_bound_.end());
+        return key;
+    }
+    Captured& captured_for_binding() {
+        std::vector<void*> key = binding_key();
+        auto it = captured_.find(key);
+        if (it == captured_.end()) {
+            if (captured_.size() >= kMaxCapturedBindings) drop_graph();
+            it = captured_.emplace(std::move(key), Captured{}).first;
+        }
+        return it->second;
+    }
+
+    // Destroys every captured graph, after the device has finished whatever
+    // of them was launched (a graph may be in flight on any stream).
     void drop_graph() {
-        if (graph_exec_) mchip_graph_exec_destroy(graph_exec_);
-        if (graph_steps_exec_) mchip_graph_exec_destroy(graph_steps_exec_);
-        graph_exec_ = graph_steps_exec_ = nullptr;
+        if (graphs_launched_) (void)mchip_device_synchronize();
+        graphs_launched_ = false;
+        for (auto& kv : captured_) {
+            if (kv.second.one) mchip_graph_exec_destroy(kv.second.one);
+            if (kv.second.run) mchip_graph_exec_destroy(kv.second.run);
+        }
+        captured_.clear();
     }
 
     NodeId a_of(const Launch& l) const { return graph_.node(l.node).inputs[0]; }
@@ -831,8 +876,8 @@ private:
     MemoryPlan plan_;
     DeviceInfo device_;
     void* stream_ = nullptr;
-    void* graph_exec_ = nullptr;  // graph_replay: the captured enqueue
-    void* graph_steps_exec_ = nullptr;  // graph_replay: kGraphSteps captured enqueues
+    std::map<std::vector<void*>, Captured> captured_;
+    bool graphs_launched_ = false;  // since the last drop_graph
     void* arena_ = nullptr;
     std::size_t arena_bytes_ = 0;
     std::vector<std::size_t> offset_;    // per node: arena offset

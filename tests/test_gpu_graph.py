@@ -4,7 +4,8 @@ with eager uploads and synchronisations between replays, must equal an
 executable that launches directly, bit for bit, and the CPU oracle within
 the graph's tolerance (rtol 1e-5 plus 1e-5 of the scale for elementwise
 graphs, 1e-4 with FP32 GEMMs, the tensor-core bound's scale for bf16);
-binding other buffers captures again. (The reference runs graphs only
+binding other buffers captures a graph for that binding, kept beside
+the others so that buffer sets can rotate. (The reference runs graphs only
 around its GEMM timing, bench/bench_cuda.cpp:445-493; replaying a whole
 enqueue is this build's.)"""
 
@@ -68,3 +69,37 @@ def test_every_graph_replay_equals_direct_launches(device, mc, oracle, name, dim
         replay.enqueue()
         replay.synchronize()
         assert np.array_equal(out.download().view(np.uint32), want[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("name,dims,opts,rtol", CASES[:2])
+def test_replay_over_rotating_buffer_sets_equals_direct_launches(device, mc, oracle, name, dims, opts, rtol):
+    # graph=1 with enqueue_steps over two buffer sets: each step binds its
+    # set, so a graph is captured per set and replayed when the set comes
+    # round again; rebinding never destroys a graph that may still run.
+    # Every set's output, after 2, 5 and 1 steps, must equal direct launches
+    # on that set's inputs, bit for bit.
+    print(f"case graph sets {name} {dims} {opts}", flush=True)
+    direct = mc.Compiled(path=mc.graph_path(name), dims=dims, options=opts)
+    replay = mc.Compiled(path=mc.graph_path(name), dims=dims, options={**opts, "graph": 1})
+    inputs = [uniform_inputs(oracle, direct.input_sizes, 60 + s) for s in range(2)]
+    want = [direct.run(x) for x in inputs]
+    bufs = []
+    for x in inputs:
+        ins = [mc.DeviceBuffer.from_array(a) for a in x]
+        outs = [mc.DeviceBuffer(4 * n) for n in replay.output_sizes]
+        bufs.append((ins, outs))
+    sets = [([b.ptr for b in ins], [b.ptr for b in outs]) for ins, outs in bufs]
+    for steps in (2, 5, 1):
+        for _, outs in bufs:
+            for b in outs:
+                b.fill_bytes(0xFF)
+        replay.enqueue_steps(steps, sets=sets)
+        replay.synchronize()
+        for s in range(min(steps, 2)):
+            got = [b.download() for b in bufs[s][1]]
+            for g, w in zip(got, want[s]):
+                assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"set {s} after {steps} steps"
+    cpu = oracle.evaluate_compiled(direct, inputs[0])
+    got = [b.download() for b in bufs[0][1]]
+    for g, c in zip(got, cpu):
+        assert_close(g, c, rtol, rtol * max(1.0, max_abs(c)), "against the oracle")

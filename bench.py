@@ -484,7 +484,8 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
         t = time_gemm(mc, launches, steps, warmup)
         ms = t["graph"]["ms"]
         flop = 2.0 * m * n * k
-        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits, "operand_sets": len(sets), "ms": ms,
+        e = {"m": m, "n": n, "k": k, "kernel": kernel, "splits": splits,
+             "k_ranges": mc.matmul_k_ranges(kernel, m, n, k, splits), "operand_sets": len(sets), "ms": ms,
              "ms_range": t["graph"]["ms_range"], "timed_launches": t["timed_steps"],
              "timing": "hip graph of back-to-back launches",
              "ms_direct_launches": t["direct"]["ms"], "tflops": flop / (ms * 1e-3) / 1e12}
@@ -527,7 +528,8 @@ def bench_gemm_fp32(mc, cus: int, shapes, steps: int, warmup: int) -> list[dict]
             log(f"gemm fp32 {m}x{n}x{k} autotuned ({e['autotuned']['launch']}): {tms:.4f} ms "
                 f"{e['autotuned']['tflops']:.1f} TFLOP/s")
         out.append(e)
-        log(f"gemm fp32 {m}x{n}x{k} {kernel} splits={splits}: {ms:.4f} ms {e['tflops']:.1f} TFLOP/s "
+        log(f"gemm fp32 {m}x{n}x{k} {kernel} splits={splits} ({e['k_ranges']} K ranges ran): {ms:.4f} ms "
+            f"{e['tflops']:.1f} TFLOP/s "
             f"(direct launches {t['direct']['ms']:.4f} ms), {n_sets} operand sets")
     return out
 
@@ -884,6 +886,8 @@ def summary_configs(cfgs: dict) -> dict:
         for e in cfgs["gemm_fp32"]:
             r = {"value": _r(e["tflops"]), "frac": _r(e["frac"], 3), "graph": _r(e["graph"]["tflops"]),
                  "cpu": _r(e["cpu_baseline"]["value"]) if "cpu_baseline" in e else None}
+            if e.get("splits", 1) > 1:
+                r["splits"] = [e.get("k_ranges"), e["splits"]]  # K ranges that ran, of the split count asked for
             if "gbs" in e:
                 r.update({"gbs": _r(e["gbs"]), "frac_hbm": _r(e["frac_hbm"], 3), "graph_gbs": _r(e["graph"]["gbs"])})
             rows[f"{e['m']}x{e['n']}x{e['k']}"] = r

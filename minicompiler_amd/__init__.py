@@ -109,6 +109,7 @@ _SIGNATURES = {
     "mc_split_k_splits": (_i, [_i, _i, _i, _i, _i]),
     "mc_matmul_splits": (_i, [_i, _i, _i, _i, _i]),
     "mc_matmul_workspace_bytes": (_ll, [_i, _i, _i, _i]),
+    "mc_matmul_k_ranges": (_i, [_i, _i, _i, _i, _i]),
     "mc_resolve_matmul_kernel": (_i, [_i, _i, _i, _i, _i]),
     "mc_matmul_kernel_name": (_cp, [_i]),
     "mc_matmul_kernel_from_name": (_i, [_cp]),
@@ -636,6 +637,12 @@ def split_k_splits(m: int, n: int, k: int, cu_count: int, blocks_per_cu: int = 2
 def matmul_splits(kernel: int | str, m: int, n: int, k: int, cu_count: int) -> int:
     kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
     return library().mc_matmul_splits(kid, m, n, k, cu_count)
+
+
+def matmul_k_ranges(kernel: int | str, m: int, n: int, k: int, splits: int) -> int:
+    """The K ranges launch_matmul runs given `splits` (an upper bound: the
+    narrow-tile body of split_k may run fewer)."""
+    return int(library().mc_matmul_k_ranges(matmul_kernel_id(kernel), m, n, k, splits))
 
 
 def matmul_workspace_bytes(kernel: int | str, m: int, n: int, splits: int) -> int:

@@ -861,6 +861,10 @@ MC_API int mc_matmul_splits(int kernel, int m, int n, int k, int cu_count) {
     return hip::matmul_splits(static_cast<hip::MatmulKernel>(kernel), m, n, k, cu_count);
 }
 
+MC_API int mc_matmul_k_ranges(int kernel, int m, int n, int k, int splits) {
+    return mchip_matmul_k_ranges(kernel, m, n, k, splits, MCHIP_RING_NONE);
+}
+
 MC_API long long mc_matmul_workspace_bytes(int kernel, int m, int n, int splits) {
     return static_cast<long long>(hip::matmul_workspace_bytes(static_cast<hip::MatmulKernel>(kernel), m, n, splits));
 }

@@ -113,6 +113,15 @@ int mchip_launch_narrow(const float* a, const float* b, float* c, int m, int n, 
 int mchip_launch_matmul_cfg(int kernel, const float* a, const float* b, float* c, int m, int n, int k, void* stream,
                             int splits, float* workspace, int ring_cfg);
 
+/* The number of K ranges mchip_launch_matmul_cfg runs for `kernel` when
+ * given `splits` (16-byte aligned operands, a workspace): `splits` is an
+ * upper bound, since the narrow-tile body of split_k runs fewer ranges when
+ * its plan fills the CUs with fewer (256x256x16384 with 64 splits runs 8);
+ * 1 for kernels that do not split; 0 for invalid sizes or a configuration
+ * that cannot run the product. */
+int mchip_matmul_k_ranges(int kernel, int m, int n, int k, int splits, int ring_cfg);
+int mchip_tensor_core_k_ranges(int k, int splits);
+
 /* mchip_launch_matmul_cfg for split_k that adds the K splits' partials in
  * the GEMM launch itself where the ring or narrow body runs the product: the
  * last block to finish a split of a C tile adds the tile's partials in split

@@ -613,6 +613,19 @@ extern "C" int mchip_launch_matmul_cfg(int kernel, const float* a, const float* 
     }
 }
 
+extern "C" int mchip_matmul_k_ranges(int kernel, int m, int n, int k, int splits, int ring_cfg) {
+    if (m < 1 || n < 1 || k < 1) return 0;
+    switch (kernel) {
+        case kSplitK: {
+            const MfmaPlan p = plan_mfma_f32(true, true, true, true, true, true, m, n, k, splits, ring_cfg, true);
+            return p.status == hipSuccess ? p.depth : 0;
+        }
+        case kTensorCoreBf16:
+        case kTensorCoreF16: return mchip_tensor_core_k_ranges(k, splits);
+        default: return 1;
+    }
+}
+
 extern "C" unsigned long long mchip_split_counter_bytes(int m, int n) {
     if (m < 1 || n < 1) return 0;
     // The smallest tiles of any body that folds (16x32 narrow tiles).

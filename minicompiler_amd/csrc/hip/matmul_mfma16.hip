@@ -347,6 +347,12 @@ extern "C" int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, co
     return hipErrorInvalidValue;
 }
 
+extern "C" int mchip_tensor_core_k_ranges(int k, int splits) {
+    if (k < 1) return 0;
+    const int k_split = split_len(k, splits, kBK);
+    return std::max(1, (k + k_split - 1) / k_split);
+}
+
 extern "C" unsigned mchip_mfma16_fast_grid(int m, int n, int cu_count) {
     const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
     const long long rest = cu_count > 0 ? tiles % cu_count : 0;

@@ -132,3 +132,22 @@ def test_short_k_products_run_on_the_tile_shape_that_gives_most_cus_a_tile(devic
     # The MLP at B=1024: GEMM1 (1024x2048x512) on 64x64 tiles, two per CU.
     mlp = "\n".join(mc.Compiled(path=mc.graph_path("mlp_gelu"), dims={"B": 1024}, options=opts).kernel_sources)
     assert "mc_gemm_f32_narrow<McNarrow64>" in mlp
+
+
+@pytest.mark.parametrize("m,k,n,splits,ranges", [(256, 16384, 256, 64, 8), (16, 4096, 4096, 8, 4),
+                                                 (1024, 1024, 1024, 4, 1), (2048, 2048, 2048, 1, 1)])
+def test_the_k_ranges_that_run_are_reported(device, mc, m, k, n, splits, ranges):
+    # The split count is an upper bound for the narrow-tile body: the query,
+    # the compiled graph's launch name and the plan agree on what runs.
+    print(f"case k ranges {m}x{k}x{n} splits={splits}", flush=True)
+    kernel = "split_k" if splits > 1 else "double_buffered"
+    assert mc.matmul_k_ranges(kernel, m, n, k, splits) == ranges
+    c = mc.Compiled(f"graph g\ninput a : f32[{m}, {k}]\ninput b : f32[{k}, {n}]\nc = matmul a, b\noutput c\n",
+                    options={"matmul": kernel, "split_fold": 0})
+    (name,) = [nm for nm in c.launch_names if nm.startswith("matmul")]
+    if splits == 1:
+        assert "splits=" not in name, name
+    elif ranges == splits:
+        assert f"splits={ranges}" in name and " of " not in name, name
+    else:
+        assert f"splits={ranges} of {splits}" in name, name

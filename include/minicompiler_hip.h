@@ -201,9 +201,8 @@ MC_API int mc_launch_matmul_cfg(int kernel, const float* a, const float* b, floa
                                 void* stream, int splits, float* workspace, int ring_cfg);
 /* mc_launch_matmul without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). No counterpart in the reference, whose
- * callers pass the workspace (launch_matmul, matmul_kernels.hpp:45-52). The
- * split-K partials go to a per-GPU scratch array of mc_noalloc_scratch_bytes()
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * The split-K partials go to a per-GPU scratch array of mc_noalloc_scratch_bytes()
  * (32 MiB) inside the library, held until the process ends; nothing is
  * allocated per call. A product whose partials (splits x m x n floats for
  * split_k and the tensor-core kernels with splits > 1) exceed it is refused
@@ -224,6 +223,13 @@ MC_API int mc_convert_f32(int dtype, const float* in, void* out, size_t count, v
 MC_API int mc_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
 MC_API int mc_split_k_splits(int m, int n, int k, int cu_count, int blocks_per_cu); /* matmul_kernels.hpp:11-17 */
 MC_API int mc_matmul_splits(int kernel, int m, int n, int k, int cu_count);         /* matmul_kernels.hpp:23-25 */
+/* The K ranges mc_launch_matmul actually runs when given `splits`
+ * (16-byte aligned operands, a workspace). No counterpart in the reference,
+ * whose split count is exact: here `splits` (and the workspace sized for it)
+ * is an upper bound, and split_k's narrow-tile body runs fewer ranges when
+ * fewer fill the GPU (256x256x16384 with 64 splits: 8). 1 for kernels that do
+ * not split, 0 for invalid sizes. */
+MC_API int mc_matmul_k_ranges(int kernel, int m, int n, int k, int splits);
 MC_API long long mc_matmul_workspace_bytes(int kernel, int m, int n, int splits);   /* matmul_kernels.hpp:27-30 */
 MC_API int mc_resolve_matmul_kernel(int kernel, int m, int n, int k, int cu_count); /* cuda_backend.hpp:45-49 */
 MC_API const char* mc_matmul_kernel_name(int kernel);                               /* cuda_backend.hpp:39 */

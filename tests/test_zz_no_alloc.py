@@ -3,7 +3,15 @@ the library's per-GPU scratch array, for callers that cannot allocate)
 against mc_launch_matmul with a caller workspace, through the C ABI: the
 same kernels, so the same bits. Each case makes two calls in a row on the
 shared array, the second on a smaller product, and a product whose partials
-exceed the array is refused with a message."""
+exceed the array is refused with a message. The first call of a process
+(the one that looks up the array's device address) can be captured into a
+HIP graph: checked in a child process, so that it is that process's first.
+"""
+
+import os
+import subprocess
+import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -58,3 +66,42 @@ def test_noalloc_matmul_refuses_partials_beyond_its_scratch(device, mc, oracle):
         mc.launch_matmul_noalloc("split_k", da.ptr, db.ptr, dc.ptr, m, n, 4096, None, splits)
     mc.synchronize()
     assert np.all(np.isnan(dc.download())), "a refused call must not launch"
+
+
+REPO = Path(__file__).resolve().parents[1]
+SCRIPT = r"""
+import sys
+import numpy as np
+sys.path.insert(0, {repo!r})
+import minicompiler_amd as mc
+m, k, n, splits = 256, 4096, 256, 8
+a, b = mc.uniform(m * k, 5, -1.0, 1.0), mc.uniform(k * n, 6, -1.0, 1.0)
+da, db = mc.DeviceBuffer.from_array(a), mc.DeviceBuffer.from_array(b)
+nan = np.full(m * n, np.nan, dtype=np.float32)
+c_na, c_ws = mc.DeviceBuffer.from_array(nan), mc.DeviceBuffer.from_array(nan)
+ws = mc.DeviceBuffer(mc.matmul_workspace_bytes("split_k", m, n, splits))
+s = mc.Stream()
+print("capturing the first no-allocation call", flush=True)
+g = mc.CapturedGraph(s, lambda st: mc.launch_matmul_noalloc("split_k", da.ptr, db.ptr, c_na.ptr, m, n, k, st, splits))
+mc.launch_matmul("split_k", da.ptr, db.ptr, c_ws.ptr, m, n, k, None, splits, ws.ptr)
+mc.synchronize()
+want = c_ws.download().view(np.uint32)
+for rep in range(3):
+    c_na.upload(nan)
+    g.launch()
+    s.synchronize()
+    got = c_na.download()
+    assert not np.any(np.isnan(got)), f"replay {{rep}}: an element of C was not written"
+    assert np.array_equal(got.view(np.uint32), want), f"replay {{rep}}: bits differ"
+    mc.launch_matmul("split_k", da.ptr, db.ptr, c_ws.ptr, m, n, k, None, splits, ws.ptr)
+    mc.synchronize()
+print("capture ok", flush=True)
+"""
+
+
+def test_the_first_noalloc_call_can_be_captured_into_a_graph(device):
+    print("case noalloc first call under capture (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", SCRIPT.format(repo=str(REPO))], env=dict(os.environ),
+                       capture_output=True, text=True, timeout=150)
+    assert r.returncode == 0, r.stdout[-1000:] + r.stderr[-2000:]
+    assert "capture ok" in r.stdout

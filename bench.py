@@ -346,6 +346,76 @@ def bench_elementwise_graph(mc, name: str, dims: dict, make_input, steps: int, w
             "host_us_per_step": t["host_us_per_step"], "gbs": k["gbs"], "frac": k["frac"]}
 
 
+# Child process of bench_copy_ceiling: PyTorch's copy_ of `nbytes` over
+# `sets` rotating tensor pairs, after `warm` seconds of copies, timed with
+# torch events over at least `min_ms` of copies in `runs` runs (median).
+TORCH_COPY_CHILD = r"""
+import json, math, statistics, sys, time
+import torch
+nbytes, sets, warm, min_ms, runs = int(sys.argv[1]), int(sys.argv[2]), float(sys.argv[3]), float(sys.argv[4]), int(sys.argv[5])
+if not torch.cuda.is_available():
+    sys.exit("torch sees no GPU")
+xs = [(torch.empty(nbytes // 4, device="cuda").uniform_(), torch.empty(nbytes // 4, device="cuda")) for _ in range(sets)]
+def burst(n):
+    for i in range(n):
+        x, y = xs[i % sets]
+        y.copy_(x)
+until = time.perf_counter() + warm
+while time.perf_counter() < until:
+    burst(20)
+    torch.cuda.synchronize()
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+e0.record(); burst(20); e1.record(); torch.cuda.synchronize()
+reps = max(20, int(math.ceil(min_ms / max(e0.elapsed_time(e1) / 20, 1e-4))))
+ts = []
+for _ in range(runs):
+    e0.record(); burst(reps); e1.record(); torch.cuda.synchronize()
+    ts.append(e0.elapsed_time(e1) / reps)
+ms = statistics.median(ts)
+print(json.dumps({"ms": ms, "ms_range": [min(ts), max(ts)], "gbs": 2 * nbytes / (ms * 1e-3) / 1e9,
+                  "copies_timed": reps, "torch": torch.__version__}))
+"""
+
+
+def bench_copy_ceiling(mc, steps: int, warmup: int, nbytes: int = 128 << 20) -> dict:
+    """Streaming ceilings measured beside the generated kernels: a copy of
+    `nbytes` (read once, written once) by (1) the generated copy_neg kernel
+    (graphs/copy_neg.mcg, y = -x, the same size), (2) the HIP runtime's own
+    device-to-device copy (hipMemcpyAsync, the runtime's blit kernel) and
+    (3) PyTorch's copy_, in a child process (TORCH_COPY_CHILD), when torch
+    is installed and sees the GPU. Each rotates over buffer
+    pairs past the MALL and times at least MIN_TIMED_MS of back-to-back work;
+    GB/s counts the bytes read plus the bytes written."""
+    out = {"bytes_each_way": nbytes}
+    rows = nbytes // (4 * 4096)
+    k = bench_elementwise_graph(mc, "copy_neg", {"M": rows, "N": 4096}, lambda n: mc.uniform(n, 1, -1.0, 1.0),
+                                steps, warmup)
+    out["mc_copy_neg"] = {"ms": k["kernel"]["ms"], "gbs": k["gbs"], "launch": k["kernel"]["launch"]}
+    pairs = [(mc.DeviceBuffer(nbytes), mc.DeviceBuffer(nbytes)) for _ in range(rotation_sets(2 * nbytes))]
+    for src, _ in pairs:
+        src.fill_bytes(0x3c)
+    launches = [lambda st, s=s_, d=d_: mc.memcpy_dtod_async(d.ptr, s.ptr, nbytes, st) for s_, d_ in pairs]
+    t = time_gemm(mc, launches, 20, 2)
+    for mode in ("graph", "direct"):
+        out[f"hip_memcpy_dtod_{mode}"] = {"ms": t[mode]["ms"], "gbs": 2 * nbytes / (t[mode]["ms"] * 1e-3) / 1e9}
+    del pairs, launches
+    # PyTorch ships its own HIP runtime under the same soname; in this
+    # process the library's is loaded, so PyTorch runs in a child process.
+    import subprocess
+    try:
+        proc = subprocess.run([sys.executable, "-c", TORCH_COPY_CHILD, str(nbytes), str(rotation_sets(2 * nbytes)),
+                               str(WARM_SECONDS), str(MIN_TIMED_MS), str(RUNS)],
+                              capture_output=True, text=True, timeout=300)
+        res = [json.loads(l) for l in proc.stdout.splitlines() if l.startswith("{")]
+        if proc.returncode == 0 and res:
+            out["torch_copy_"] = res[-1]
+        else:
+            out["torch_copy_error"] = (proc.stderr or proc.stdout)[-300:]
+    except (OSError, subprocess.TimeoutExpired) as e:
+        out["torch_copy_error"] = str(e)[:300]
+    return out
+
+
 def bench_fusion(mc, dims: dict, rounds: int = 40) -> dict:
     """The reference's fusion comparison (bench/bench_cuda.cpp:182-288): the
     GELU chain compiled unfused (passes dne,fold,dne: one launch per op) and
@@ -778,6 +848,11 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
     """BASELINE's other configs, each with its CPU baseline from `cpu`."""
     cfgs = line.setdefault("configs", {})
     want = lambda w: args.workload == w or (args.workload == "mlp" and not args.quick)
+    if want("gelu") or want("batchnorm"):
+        cc = bench_copy_ceiling(mc, args.steps, args.warmup)
+        cfgs["copy_ceiling_128MiB"] = cc
+        log("copy ceiling (128 MiB each way): " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in cc.items()
+                                                             if isinstance(v, dict)))
     if want("gelu"):
         e = bench_elementwise_graph(mc, "gelu_chain", {"M": 4096, "N": 4096}, lambda n: mc.uniform(n, 1, -3.0, 3.0),
                                     args.steps, args.warmup)
@@ -869,6 +944,9 @@ def summary_configs(cfgs: dict) -> dict:
             e = cfgs[name]
             out[name] = {"value": _r(e["gbs"]), "unit": "GB/s", "frac": _r(e["frac"], 3),
                          "cpu": _cpu_short(e.get("cpu_baseline"))}
+    if "copy_ceiling_128MiB" in cfgs:
+        out["copy_ceiling_128MiB"] = {k: _r(v["gbs"]) for k, v in cfgs["copy_ceiling_128MiB"].items()
+                                      if isinstance(v, dict)}
     if "gelu_fusion_4096x4096" in cfgs:
         f = cfgs["gelu_fusion_4096x4096"]
         out["gelu_fusion_4096x4096"] = {
@@ -1017,6 +1095,8 @@ def main() -> int:
                      "config": {"workload": "copy_neg (counter calibration)", **k["dims"]},
                      "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],
                                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"], "traffic": None}})
+        if not args.quick:
+            line.setdefault("configs", {})["copy_ceiling_128MiB"] = bench_copy_ceiling(mc, args.steps, args.warmup)
     elif args.workload in ("gelu", "batchnorm"):
         k = next(iter(cfgs.values()))
         line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",

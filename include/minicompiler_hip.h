@@ -243,6 +243,9 @@ MC_API int mc_device_malloc(void** ptr, size_t bytes);
 MC_API int mc_device_free(void* ptr);
 MC_API int mc_memcpy_htod(void* dst, const void* src, size_t bytes);
 MC_API int mc_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy enqueued on `stream` (the HIP runtime's own copy,
+ * hipMemcpyAsync; no wait). Used as an independent HBM streaming ceiling. */
+MC_API int mc_memcpy_dtod_async(void* dst, const void* src, size_t bytes, void* stream);
 MC_API int mc_memset(void* dst, int value, size_t bytes);
 MC_API int mc_device_synchronize(void);
 MC_API int mc_stream_create(void** stream);

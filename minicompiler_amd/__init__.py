@@ -119,6 +119,7 @@ _SIGNATURES = {
     "mc_device_free": (_i, [_vp]),
     "mc_memcpy_htod": (_i, [_vp, _vp, _sz]),
     "mc_memcpy_dtoh": (_i, [_vp, _vp, _sz]),
+    "mc_memcpy_dtod_async": (_i, [_vp, _vp, _sz, _vp]),
     "mc_memset": (_i, [_vp, _i, _sz]),
     "mc_device_synchronize": (_i, []),
     "mc_stream_create": (_i, [_c.POINTER(_vp)]),
@@ -619,6 +620,11 @@ def launch_matmul_lowp(kernel: int | str, dtype: int, a: int, b: int, c: int, m:
     kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
     _check(library().mc_launch_matmul_lowp(kid, dtype, a, b, c, m, n, k, _stream_handle(stream), splits, workspace),
            f"launch_matmul_lowp({matmul_kernel_name(kid)})")
+
+
+def memcpy_dtod_async(dst: int, src: int, nbytes: int, stream=None) -> None:
+    """The HIP runtime's device-to-device copy (hipMemcpyAsync), enqueued on `stream`."""
+    _check(library().mc_memcpy_dtod_async(dst, src, nbytes, _stream_handle(stream)), "hipMemcpyAsync D2D")
 
 
 def convert_f32(dtype: int, src: int, dst: int, count: int, stream=None) -> None:

@@ -895,6 +895,9 @@ MC_API int mc_memcpy_htod(void* dst, const void* src, size_t bytes) {
     return rc ? rc : mchip_stream_synchronize(nullptr);
 }
 MC_API int mc_memcpy_dtoh(void* dst, const void* src, size_t bytes) { return mchip_memcpy_dtoh(dst, src, bytes); }
+MC_API int mc_memcpy_dtod_async(void* dst, const void* src, size_t bytes, void* stream) {
+    return mchip_memcpy_dtod_async(dst, src, bytes, stream);
+}
 MC_API int mc_memset(void* dst, int value, size_t bytes) {
     const int rc = mchip_memset_async(dst, value, bytes, nullptr);
     return rc ? rc : mchip_stream_synchronize(nullptr);

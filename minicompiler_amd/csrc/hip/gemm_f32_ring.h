@@ -123,43 +123,64 @@ using McRingMid = McRingCfg<64, 128, 32, 64, 4, 3>;
 __device__ __forceinline__ int mc_ring_min(int a, int b) { return a < b ? a : b; }
 
 // Where this lane's fetches of one step come from, for one unit (a tile, or
-// a tile's share of K under split-K).
+// a tile's share of K under split-K): buffer resources based at the unit's
+// origin in A (row row0, column kb) and in B (row kb, column col0), the
+// lane's byte offset from each origin for its chunks of step 0, and the
+// bytes between consecutive K steps (kBK * 4 in A, kBK rows in B), which go
+// in the scalar offset. A buffer load takes its per-lane address as a
+// 32-bit offset added to a base held in scalar registers, so no vector
+// instruction computes addresses in the main loop (the 64-bit global
+// addresses it replaces took one VALU add per load; 8192x512x2048 ran 4%
+// slower so). The host guarantees that every offset fits in 31 bits
+// (mchip_ring_offsets_fit).
 template <class Cfg>
 struct McRingFetch {
-    const float* a_src[Cfg::kFA];
-    const float* b_src[Cfg::kFB];
-    long long b_step;  // elements between consecutive K steps of B
+    __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+    int a_off[Cfg::kFA];
+    int b_off[Cfg::kFB];
+    int b_step;
 };
 
 struct McRingUnit {
     int row0, col0, kb, steps, split;
 };
 
-// Global -> LDS without registers: global_load_lds_dwordx4 writes lane l's
-// 16 bytes at (LDS base + 16 l). Instruction idx of a step's fetch: A
-// blocks first, then B blocks.
+// Raw buffer resource over `base` (stride 0: byte-addressed; the offsets
+// stay inside the operand, so the range is not what bounds them).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mc_ring_rsrc(const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// Global -> LDS without registers: buffer_load_dwordx4 ... lds writes lane
+// l's 16 bytes at (LDS base + 16 l). (A plain function: called in a
+// template, the builtin failed the host pass of the AOT build.)
+__device__ __forceinline__ void mc_ring_buffer_to_lds(__amdgpu_buffer_rsrc_t rsrc, MC_RING_LDS unsigned char* dst,
+                                                      int voffset, int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, reinterpret_cast<MC_RING_LDS void*>(dst), 16, voffset, soffset, 0, 0);
+}
+
+// Instruction idx of a step's direct fetch: A blocks first, then B blocks.
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_fetch_one(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
                                                   int t, int idx) {
     if (idx < Cfg::kFA) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.a_src[idx] + t * Cfg::kBK),
-                                         reinterpret_cast<MC_RING_LDS void*>(wr + (wave * Cfg::kFA + idx) * 1024), 16, 0,
-                                         0);
+        mc_ring_buffer_to_lds(f.a_rsrc, wr + (wave * Cfg::kFA + idx) * 1024, f.a_off[idx], t * (Cfg::kBK * 4));
     } else {
         const int i = idx - Cfg::kFA;
-        __builtin_amdgcn_global_load_lds(
-            static_cast<const void*>(f.b_src[i] + t * f.b_step),
-            reinterpret_cast<MC_RING_LDS void*>(wr + Cfg::kABytes + (wave * Cfg::kFB + i) * 1024), 16, 0, 0);
+        mc_ring_buffer_to_lds(f.b_rsrc, wr + Cfg::kABytes + (wave * Cfg::kFB + i) * 1024, f.b_off[i], t * f.b_step);
     }
 }
 
-// The staged fetch: instruction idx of a step as a 16-byte global load into
+// The staged fetch: instruction idx of a step as a 16-byte buffer load into
 // registers, and later the store of those registers to the LDS position the
 // direct load would fill (so both fetch forms give the same stage contents).
 template <class Cfg>
 __device__ __forceinline__ mc_ring_f32x4 mc_ring_load_one(const McRingFetch<Cfg>& f, int t, int idx) {
-    if (idx < Cfg::kFA) return *reinterpret_cast<const mc_ring_f32x4*>(f.a_src[idx] + t * Cfg::kBK);
-    return *reinterpret_cast<const mc_ring_f32x4*>(f.b_src[idx - Cfg::kFA] + t * f.b_step);
+    if (idx < Cfg::kFA)
+        return __builtin_bit_cast(mc_ring_f32x4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(f.a_rsrc, f.a_off[idx], t * (Cfg::kBK * 4), 0));
+    return __builtin_bit_cast(mc_ring_f32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(f.b_rsrc, f.b_off[idx - Cfg::kFA], t * f.b_step, 0));
 }
 
 template <class Cfg>
@@ -170,22 +191,24 @@ __device__ __forceinline__ void mc_ring_store_one(MC_RING_LDS unsigned char* wr,
     *reinterpret_cast<MC_RING_LDS mc_ring_f32x4*>(wr + blk + 16 * lane) = v;
 }
 
-// All of a step's fetch instructions (the prologue's).
+// All of a step's fetch instructions (the prologue's): direct loads, or for
+// the staged configurations the loads into registers and their LDS stores
+// (so a staged kernel issues no direct load at all, and the compiler's
+// count of loads in flight at the main loop stays exact: with a direct load
+// possibly in flight it waited for every load before each LDS store).
 template <class Cfg>
 __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, const McRingFetch<Cfg>& f, int wave,
                                               int t) {
-    MC_RING_LDS unsigned char* sa = wr + wave * Cfg::kFA * 1024;
-    MC_RING_LDS unsigned char* sb = wr + Cfg::kABytes + wave * Cfg::kFB * 1024;
+    if constexpr (Cfg::kStaged) {
+        const int lane = static_cast<int>(threadIdx.x) & 63;
+        mc_ring_f32x4 v[Cfg::kFetch];
 #pragma unroll
-    for (int i = 0; i < Cfg::kFA; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.a_src[i] + t * Cfg::kBK),
-                                         reinterpret_cast<MC_RING_LDS void*>(sa + i * 1024), 16, 0, 0);
-    }
-    const long long bo = t * f.b_step;
+        for (int idx = 0; idx < Cfg::kFetch; ++idx) v[idx] = mc_ring_load_one<Cfg>(f, t, idx);
 #pragma unroll
-    for (int i = 0; i < Cfg::kFB; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(f.b_src[i] + bo),
-                                         reinterpret_cast<MC_RING_LDS void*>(sb + i * 1024), 16, 0, 0);
+        for (int idx = 0; idx < Cfg::kFetch; ++idx) mc_ring_store_one<Cfg>(wr, wave, lane, idx, v[idx]);
+    } else {
+#pragma unroll
+        for (int idx = 0; idx < Cfg::kFetch; ++idx) mc_ring_fetch_one<Cfg>(wr, f, wave, t, idx);
     }
 }
 
@@ -200,11 +223,15 @@ __device__ __forceinline__ void mc_ring_fetch(MC_RING_LDS unsigned char* wr, con
 // keep the compiler from making them wait for the fetch.
 //
 // The 16 groups (q, e) of a step each take one B read (and, at e = 0, the
-// K group's A reads). The reads of group t + 1 are issued before the MFMAs
-// of group t, into the other of two register sets, and a scheduling barrier
-// keeps them there: the MFMAs of group t then cover the LDS latency of group
-// t + 1 (left to itself the compiler reuses one register set and waits for
-// each read right before its MFMAs).
+// K group's A reads). The reads of group t + 1 are issued with the MFMAs of
+// group t, into the other of two register sets: the MFMAs of group t then
+// cover the LDS latency of group t + 1 (left to itself the compiler reuses
+// one register set and waits for each read right before its MFMAs). Within
+// a group the memory instructions are interleaved with the MFMAs, one of
+// each kind (LDS write, load, LDS read) after each MFMA, so each issues while
+// an MFMA runs: issued as one block between two groups' MFMAs, they left the
+// matrix unit idle while the wave issued them (8192x512x2048 on the wide
+// configuration: 126.2 us so, 122.9 us interleaved, one MI355X).
 //
 // Staged configurations: the registers loaded one step ago are written to
 // `wr`, and the next fetch is loaded into the same registers right behind
@@ -252,13 +279,19 @@ __device__ __forceinline__ void mc_ring_step(const MC_RING_LDS unsigned char* __
             }
             bv[(t + 1) & 1] = *reinterpret_cast<const MC_RING_LDS BT*>(rd + b_off + (t + 1) * Cfg::kBRow);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < Cfg::kAI; ++i)
 #pragma unroll
             for (int j = 0; j < Cfg::kBJ; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q & 1][i][e], BV::get(bv[t & 1], j), acc[i][j], 0,
                                                                  0, 0);
+#pragma unroll
+        for (int r = 0; r < Cfg::kAI * Cfg::kBJ; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // an LDS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a load
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // an LDS read
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -278,22 +311,6 @@ __device__ __forceinline__ void mc_ring_wait_later(int later) {
         mc_ring_wait_later<kFetch, kMax - 1>(later);
     } else {
         MC_RING_WAIT(0);
-    }
-}
-
-// Staged configurations: wait until the prologue's direct fetch of step g
-// has landed, `later` = direct fetch groups issued after it (one group of
-// staged loads, issued after all of them, is always in flight too).
-template <int kFetch, int kMax>
-__device__ __forceinline__ void mc_ring_wait_direct(int later) {
-    if constexpr (kMax > 0) {
-        if (later >= kMax) {
-            MC_RING_WAIT((kMax + 1) * kFetch);
-            return;
-        }
-        mc_ring_wait_direct<kFetch, kMax - 1>(later);
-    } else {
-        MC_RING_WAIT(kFetch);
     }
 }
 
@@ -490,23 +507,27 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
     // bb 1024 / kBRow + l / (kBRow / 16), physical chunk l % (kBRow / 16),
     // logical chunk that ^ 8 (k row / 16 % 2).
     constexpr int kLanesPerBRow = Cfg::kBRow / 16;
+    // Offsets are from the unit's origin; clamped rows and columns are at or
+    // past it (row0 <= m - 1, col0 <= n - 4).
     auto fetch_of = [&](const McRingUnit& u) {
         McRingFetch<Cfg> f;
+        f.a_rsrc = mc_ring_rsrc(a + static_cast<long long>(u.row0) * k + u.kb);
+        f.b_rsrc = mc_ring_rsrc(b + static_cast<long long>(u.kb) * n + u.col0);
 #pragma unroll
         for (int i = 0; i < Cfg::kFA; ++i) {
             const int rb = Cfg::kFA * wave + i;
             const int r = mc_ring_min(u.row0 + rb * 8 + (lane & 7), m - 1);
             const int ch = 2 * (lane >> 4) + (((lane >> 3) & 1) ^ (rb & 1));
-            f.a_src[i] = a + static_cast<long long>(r) * k + u.kb + 4 * ch;
+            f.a_off[i] = 4 * ((r - u.row0) * k + 4 * ch);
         }
 #pragma unroll
         for (int i = 0; i < Cfg::kFB; ++i) {
             const int kk = (Cfg::kFB * wave + i) * (1024 / Cfg::kBRow) + lane / kLanesPerBRow;
             const int g = (lane % kLanesPerBRow) ^ (8 * ((kk >> 4) & 1));
             const int col = mc_ring_min(u.col0 + 4 * g, n - 4);
-            f.b_src[i] = b + static_cast<long long>(u.kb + kk) * n + col;
+            f.b_off[i] = 4 * (kk * n + col - u.col0);
         }
-        f.b_step = static_cast<long long>(Cfg::kBK) * n;
+        f.b_step = 4 * Cfg::kBK * n;
         return f;
     };
 
@@ -577,13 +598,10 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
             for (int j = 0; j < Cfg::kBJ; ++j) acc[i][j] = mc_ring_f32x16{};
         for (int t = 0; t < u.steps; ++t, ++g) {
             if constexpr (Cfg::kStaged) {
-                // Step g came from the prologue's direct fetch (g < pre) or
-                // was written to LDS from registers during step g - 1 (and
-                // waited for with the LDS reads below).
-                if (g < pre)
-                    mc_ring_wait_direct<Cfg::kFetch, Cfg::kStages - 2>(pre - 1 - g);
-                else
-                    MC_RING_WAIT(63);
+                // Step g was written to LDS from registers by the prologue
+                // or during step g - 1: wait for this wave's LDS writes (and
+                // reads).
+                MC_RING_WAIT(63);
             } else {
                 // Fetch groups issued after the one of step g (stores issued
                 // after it only make the wait longer): wait for that one and

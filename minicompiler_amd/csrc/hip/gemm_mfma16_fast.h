@@ -105,16 +105,30 @@ struct FastShape {
     static constexpr int kFetch = kFetchA + 2;
 };
 
-// Per-lane addressing, set up once per block.
+// Per-lane addressing, set up once per block. The fetches are buffer loads
+// from bases at the tile's origin in A (row row0) and B (column col0): the
+// lane's 32-bit byte offset for k step 0 in a vector register, the step's
+// offset (2 k0 bytes in A, 2 k0 n in B) in a scalar one, so the memory phase
+// computes no addresses (the 64-bit global addresses it replaces took vector
+// adds and a multiply per step). The host keeps every offset below 2^31.
 template <int kRows>
 struct FastLane {
-    const unsigned short* a_src[FastShape<kRows>::kFetchA];  // A chunk this lane fetches per instruction (k offset 0)
-    const unsigned short* b_src[2];                          // B chunk (k row offset 0)
-    long long b_step;                                        // elements between consecutive K steps of B
-    int a_off[FastShape<kRows>::kRowFrags];                  // LDS byte offsets of the A fragments
-    int b_off[2][kFColFrags];                                // LDS byte offsets of the two transposed B reads
+    __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
+    int a_src[FastShape<kRows>::kFetchA];  // byte offset of the A chunk this lane fetches per instruction (k 0)
+    int b_src[2];                          // byte offset of the B chunk (k row 0)
+    int b_step;                            // bytes between consecutive K steps of B
+    int a_off[FastShape<kRows>::kRowFrags];  // LDS byte offsets of the A fragments
+    int b_off[2][kFColFrags];                // LDS byte offsets of the two transposed B reads
     int wave;
 };
+
+// One 16-byte-per-lane buffer load into LDS (lane l at dst + 16 l). A plain
+// function: called in a template, the builtin failed the host pass of the
+// ahead-of-time build.
+__device__ __forceinline__ void fast_buffer_to_lds(__amdgpu_buffer_rsrc_t rsrc, MC_LDS unsigned char* dst, int voffset,
+                                                   int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, reinterpret_cast<MC_LDS void*>(dst), 16, voffset, soffset, 0, 0);
+}
 
 template <int kRows>
 __device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastLane<kRows>& L, int fetch_k) {
@@ -122,16 +136,10 @@ __device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastL
     MC_LDS unsigned char* sa = wr + L.wave * kFA * 1024;
     MC_LDS unsigned char* sb = wr + kFBOffset + L.wave * 4 * 512;
 #pragma unroll
-    for (int i = 0; i < kFA; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.a_src[i] + fetch_k),
-                                         reinterpret_cast<MC_LDS void*>(sa + i * 1024), 16, 0, 0);
-    }
-    const long long bk = (fetch_k / kFBK) * L.b_step;
+    for (int i = 0; i < kFA; ++i) fast_buffer_to_lds(L.a_rsrc, sa + i * 1024, L.a_src[i], 2 * fetch_k);
+    const int bk = (fetch_k / kFBK) * L.b_step;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(L.b_src[i] + bk),
-                                         reinterpret_cast<MC_LDS void*>(sb + i * 1024), 16, 0, 0);
-    }
+    for (int i = 0; i < 2; ++i) fast_buffer_to_lds(L.b_rsrc, sb + i * 1024, L.b_src[i], bk);
 }
 
 template <int kRows>
@@ -214,13 +222,17 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
 
     FastLane<kRows> L;
     L.wave = wave;
+    L.a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(a) + static_cast<long long>(row0) * k, 0,
+                                                 0x7fffffff, 0x00020000);
+    L.b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(b) + col0, 0, 0x7fffffff, 0x00020000);
     // A: wave w fills the 16-row blocks kFetchA w + i, one per instruction;
-    // lane -> (row 16 (kFetchA w + i) + l % 16, chunk l / 16).
+    // lane -> (row 16 (kFetchA w + i) + l % 16, chunk l / 16). Rows past the
+    // edge are clamped, so every offset is at or past the origin.
 #pragma unroll
     for (int i = 0; i < Sh::kFetchA; ++i) {
         const int r = (wave * Sh::kFetchA + i) * 16 + (lane & 15);
         const int gr = mc_min16(row0 + r, m - 1);
-        L.a_src[i] = a + static_cast<long long>(gr) * k + (lane >> 4) * 8;
+        L.a_src[i] = 2 * ((gr - row0) * k + (lane >> 4) * 8);
     }
     // B: wave w fills k rows 4 w .. 4 w + 3, two per instruction; lane ->
     // (k row 4 w + 2 i + l / 32, physical chunk l % 32).
@@ -229,9 +241,9 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
         const int kr = wave * 4 + i * 2 + (lane >> 5);
         const int lc = (lane & 31) ^ (2 * swz_b(kr));
         const int gc = mc_min16(col0 + lc * 8, n - 8);
-        L.b_src[i] = b + static_cast<long long>(kr) * n + gc;
+        L.b_src[i] = 2 * (kr * n + gc - col0);
     }
-    L.b_step = static_cast<long long>(kFBK) * n;
+    L.b_step = 2 * kFBK * n;
     // Wave (wm, wn) of the 2x4 grid owns rows kRows / 2 wm .., columns 64 wn ...
     const int wr = (wave >> 2) * (kRows / 2), wc = (wave & 3) * 64;
     const int li = lane & 15, g = lane >> 4;

@@ -608,7 +608,7 @@ private:
             l->matmul = l->splits > 1 ? MatmulKernel::SplitK : MatmulKernel::DoubleBuffered;
         }
         const bool bf16 = l->matmul == MatmulKernel::TensorCoreBf16, f16 = l->matmul == MatmulKernel::TensorCoreF16;
-        if (options_.convert_tensor_core_operands && (bf16 || f16) && l->k % 64 == 0 && l->n % 8 == 0 && l->n >= 8) {
+        if (options_.convert_tensor_core_operands && (bf16 || f16) && mchip_mfma16_fast_fits(l->m, l->n, l->k)) {
             l->lowp = true;
             l->splits = 1;
             l->dtype = bf16 ? MCHIP_DTYPE_BF16 : MCHIP_DTYPE_F16;

@@ -36,6 +36,12 @@ int mchip_sum_split_partials(const float* partial, float* c, size_t count, int s
  * (those tiles then run as two 128-row halves). */
 unsigned mchip_mfma16_fast_grid(int m, int n, int cu_count);
 
+/* Whether the bf16/fp16 256x256-tile kernel takes an m x n x k product: K a
+ * multiple of 64, N a multiple of 8 (at least 8), and every byte offset its
+ * buffer loads take from a tile's origin below 2^31 (256 rows of A, K + 32
+ * rows of B). Alignment is the caller's to check. */
+int mchip_mfma16_fast_fits(int m, int n, int k);
+
 /* Whether gfx950 runs `kernel` (all but TensorCoreTf32). */
 int mchip_matmul_supported(int kernel);
 

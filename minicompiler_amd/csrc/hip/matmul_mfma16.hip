@@ -219,7 +219,7 @@ __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigne
 // 16-byte aligned, and no split.
 bool fast_eligible(const void* a, const void* b, const float* c, int m, int n, int k, int splits) {
     const auto al = [](const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16 == 0; };
-    return splits <= 1 && k % (2 * kFBK) == 0 && n % 8 == 0 && al(a) && al(b) && al(c) && m >= 1 && n >= 8;
+    return splits <= 1 && mchip_mfma16_fast_fits(m, n, k) && al(a) && al(b) && al(c);
 }
 
 // CUs of the current device, asked once per device.
@@ -351,6 +351,11 @@ extern "C" int mchip_tensor_core_k_ranges(int k, int splits) {
     if (k < 1) return 0;
     const int k_split = split_len(k, splits, kBK);
     return std::max(1, (k + k_split - 1) / k_split);
+}
+
+extern "C" int mchip_mfma16_fast_fits(int m, int n, int k) {
+    if (m < 1 || n < 8 || k < 1 || k % (2 * kFBK) != 0 || n % 8 != 0) return 0;
+    return 2LL * kFBM * k < (1LL << 31) && 2LL * (static_cast<long long>(k) + kFBK) * n < (1LL << 31);
 }
 
 extern "C" unsigned mchip_mfma16_fast_grid(int m, int n, int cu_count) {

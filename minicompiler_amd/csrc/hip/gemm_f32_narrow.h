@@ -94,6 +94,18 @@ using McNarrow16x32 = McNarrowCfg<1, 2, 4, 2, false>;
 // 31-36 us against 22.5 us for one block per CU in two rounds.
 using McNarrow64 = McNarrowCfg<4, 4, 4, 2, false, 96>;
 
+// A 16- or 8-byte buffer load at (voffset + soffset) from the resource's
+// base; kStream: non-temporal (the slc bit: a read-only stream reached 7.1
+// TB/s with non-temporal loads against 6.3 TB/s without on an MI355X).
+template <typename T, bool kStream>
+__device__ __forceinline__ T mc_narrow_load(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset) {
+    constexpr int kAux = kStream ? 2 : 0;
+    if constexpr (sizeof(T) == 16)
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, kAux));
+    else
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(rsrc, voffset, soffset, kAux));
+}
+
 // One batch of a wave's operands: kU groups of 16 k.
 template <class Cfg>
 struct McNarrowRegs {
@@ -141,14 +153,24 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
     const int g0 = wave * per < groups ? wave * per : groups;
     const int g1 = g0 + per < groups ? g0 + per : groups;
 
-    const float* __restrict__ ap[kRG];
+    // Operands through buffer loads: bases at the block's origin in A (row
+    // row0, column kb) and B (row kb, column col0) in scalar registers, the
+    // lane's byte offset from them in a vector register, the group's offset
+    // (64 g bytes in A, 64 g n in B) in a scalar one, so no vector
+    // instruction computes a load address (the host keeps every offset below
+    // 2^31: mchip_f32_narrow_plan).
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a) + static_cast<long long>(row0) * k + kb, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(b) + static_cast<long long>(kb) * n + col0, 0, 0x7fffffff, 0x00020000);
+    int a_off[kRG];
 #pragma unroll
     for (int r = 0; r < kRG; ++r) {
         const int row = row0 + 16 * r + cl < m ? row0 + 16 * r + cl : m - 1;
-        ap[r] = a + static_cast<long long>(row) * k + kb + 4 * s;
+        a_off[r] = 4 * ((row - row0) * k + 4 * s);
     }
-    const float* __restrict__ bp = b + static_cast<long long>(kb + 4 * s) * n + colc;
-    const long long nn = n;
+    const int b_off = 4 * (4 * s * n + colc - col0);
+    const int b_row = 4 * n;  // bytes per row of B
 
     mc_nw_f32x4 acc[kRG][kVec] = {};
     // Loads of `units` groups from group g into x, then (after a scheduling
@@ -159,16 +181,10 @@ __device__ __forceinline__ void mc_gemm_f32_narrow(const float* __restrict__ a, 
 #pragma unroll
         for (int u = 0; u < kN; ++u) {
 #pragma unroll
-            for (int r = 0; r < kRG; ++r) x.a[u][r] = *reinterpret_cast<const mc_nw_f32x4*>(ap[r] + 16 * (g + u));
+            for (int r = 0; r < kRG; ++r) x.a[u][r] = mc_narrow_load<mc_nw_f32x4, false>(a_rsrc, a_off[r], 64 * (g + u));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const BV* p = reinterpret_cast<const BV*>(bp + (16LL * (g + u) + e) * nn);
-                if constexpr (Cfg::kStreamB) {
-                    x.b[u][e] = __builtin_nontemporal_load(p);
-                } else {
-                    x.b[u][e] = *p;
-                }
-            }
+            for (int e = 0; e < 4; ++e)
+                x.b[u][e] = mc_narrow_load<BV, Cfg::kStreamB>(b_rsrc, b_off, (16 * (g + u) + e) * b_row);
         }
         __builtin_amdgcn_sched_barrier(0);
     };

@@ -460,6 +460,9 @@ extern "C" int mchip_f32_narrow_plan(int m, int n, int k, int max_splits, int cu
                                      int* splits, int* k_split) {
     *shape = *splits = *k_split = 0;
     if (m < 1 || n < 4 || n % 4 != 0 || k < 16 || k % 16 != 0 || max_splits < 1 || cu_count < 1) return 0;
+    // The narrow body's buffer loads take 31-bit byte offsets from a block's
+    // origin: up to 64 rows of A and K + 16 rows of B past it.
+    if (64LL * k * 4 >= (1LL << 31) || (static_cast<long long>(k) + 16) * n * 4 >= (1LL << 31)) return 0;
     auto tiles_of = [&](int sh) {
         return static_cast<long long>((m + mchip_narrow_rows(sh) - 1) / mchip_narrow_rows(sh)) *
                ((n + mchip_narrow_cols(sh) - 1) / mchip_narrow_cols(sh));

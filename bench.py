@@ -848,7 +848,7 @@ def run_configs(mc, args, cus: int, line: dict, cpu: dict) -> None:
     """BASELINE's other configs, each with its CPU baseline from `cpu`."""
     cfgs = line.setdefault("configs", {})
     want = lambda w: args.workload == w or (args.workload == "mlp" and not args.quick)
-    if want("gelu") or want("batchnorm"):
+    if (want("gelu") or want("batchnorm")) and not args.no_copy_ceiling:
         cc = bench_copy_ceiling(mc, args.steps, args.warmup)
         cfgs["copy_ceiling_128MiB"] = cc
         log("copy ceiling (128 MiB each way): " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in cc.items()
@@ -1034,6 +1034,8 @@ def main() -> int:
     ap.add_argument("--config-cpu-seconds", type=float, default=1.5, help="each other config's CPU baseline")
     ap.add_argument("--min-timed-ms", type=float, default=MIN_TIMED_MS,
                     help="GPU work per timed loop of the other configs (0 under rocprofv3)")
+    ap.add_argument("--no-copy-ceiling", action="store_true",
+                    help="skip the copy ceilings beside the elementwise configs (profiling runs)")
     ap.add_argument("--out", default=str(ROOT / "results" / "bench_full.json"),
                     help="file for the full record (every config's detail); '' for none")
     args = ap.parse_args()

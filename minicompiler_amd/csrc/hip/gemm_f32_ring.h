@@ -81,7 +81,10 @@ struct McRingCfg {
 // The configurations the library runs (mchip_f32_ring_plan picks one by a
 // cost model of the rounds each needs and its measured efficiency):
 //   big:  one block of 4 waves per CU, 256x256 tiles, 128x128 per wave (16
-//         accumulators, in AGPRs), 2 stages of 64 KiB, direct fetch;
+//         accumulators, in AGPRs), 2 stages of 64 KiB, direct fetch; since
+//         the staged fetch became buffer loads interleaved with the MFMAs,
+//         wide is 1-4% faster on every shape both fill, and big runs only
+//         when forced (ring=big);
 //   wide: up to two blocks of 4 waves per CU, 128x128 tiles, 64x64 per wave
 //         (accumulators in VGPRs), 2 stages, fetch staged through registers
 //         a step ahead (measured 3-7% faster than its direct-fetch form, and

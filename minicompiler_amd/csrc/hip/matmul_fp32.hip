@@ -413,9 +413,12 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
     }
     // Time in units of one 128x128 tile-split on a whole CU: the tile-splits
     // of the busiest CU x work per tile-split (a 256x256 tile is four) /
-    // efficiency (big and wide measured within 1% of each other on 8192^3,
-    // 4096^3 and the MLP's first GEMM, where both fill every CU; wide with
-    // one block per CU as efficient per tile as with two).
+    // efficiency. With the staged buffer-load fetch interleaved with the
+    // MFMAs, wide runs 1-4% faster than big where both fill every CU (bare,
+    // one MI355X: 8192^3 7528 against 7607 us, 4096^3 941 against 965,
+    // 8192x2048x512 126.6 against 131.6, 2048x8192x2048 477 against 486).
+    // With these factors the model never prefers big (a 256x256 tile round is
+    // four 128x128 tile-splits on a CU either way); big stays for ring=big.
     const long long cus = cu_count;
     if (m <= RingThin::kBM) {
         const long long t32 = static_cast<long long>((n + 127) / 128) * depth;
@@ -427,7 +430,7 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
     const long long t128 = static_cast<long long>((m + 127) / 128) * ((n + 127) / 128) * depth;
     const double big = static_cast<double>((t256 + cus - 1) / cus) * 4.0 / 0.92;
     const long long wide_grid = std::min(t128, 2 * cus);
-    const double wide = static_cast<double>((wide_grid > cus ? 2 : 1) * ((t128 + wide_grid - 1) / wide_grid)) / 0.91;
+    const double wide = static_cast<double>((wide_grid > cus ? 2 : 1) * ((t128 + wide_grid - 1) / wide_grid)) / 0.95;
     if (big <= wide) {
         *grid = static_cast<unsigned>(std::min(t256, cus));
         *block = RingBig::kThreads;

@@ -55,23 +55,28 @@ def test_ring_body_equals_the_two_stage_body_bit_for_bit(device, mc, oracle, m, 
     assert np.all(np.abs(ring.astype(np.float64) - exact) <= bound)
 
 
-@pytest.mark.parametrize("batch,config", [(4096, "McRingWide"), (8192, "McRingBig")])
-def test_fused_epilogue_on_the_ring_equals_the_two_stage_body(device, mc, oracle, batch, config):
-    # The MLP block: GEMM1 (B x 2048 x 512) runs the ring (two 128x128 blocks
-    # per CU at B=4096, 256x256 tiles at B=8192) with bias+GELU fused into
-    # its store; GEMM2 (B x 512 x 2048) the 128x128 ring with one block per
-    # CU, with b2 + residual (a fused GEMM keeps the 4-wave blocks where an
-    # unfused one would take the 8-wave block). The vectorized graph runs the
-    # two-stage body (also fused): identical bits throughout.
+@pytest.mark.parametrize("batch,ring,config", [(4096, None, "McRingWide"), (8192, None, "McRingWide"),
+                                               (8192, "big", "McRingBig")])
+def test_fused_epilogue_on_the_ring_equals_the_two_stage_body(device, mc, oracle, batch, ring, config):
+    # The MLP block: GEMM1 (B x 2048 x 512) runs the ring (128x128 tiles in
+    # two blocks per CU, as the planner picks, or 256x256 tiles when forced)
+    # with bias+GELU fused into its store; GEMM2 (B x 512 x 2048) the 128x128
+    # ring with one block per CU, with b2 + residual (a fused GEMM keeps the
+    # 4-wave blocks where an unfused one would take the 8-wave block). The
+    # vectorized graph runs the two-stage body (also fused): identical bits
+    # throughout.
+    print(f"case mlp B={batch} ring={ring}", flush=True)
     dims = {"B": batch}
-    ring = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"matmul": "double_buffered"})
+    options = {"matmul": "double_buffered"}
+    if ring:
+        options["ring"] = ring
+    ring_graph = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options=options)
     two = mc.Compiled(path=mc.graph_path("mlp_gelu"), dims=dims, options={"matmul": "vectorized"})
-    sources = "\n".join(ring.kernel_sources)
-    assert f"mc_gemm_f32_ring<{config}>" in sources, ring.launch_names
-    assert sources.count("mc_gemm_f32_ring<McRingWide>") >= 1, ring.launch_names
-    assert ring.kernel_launches == 2
-    inputs = uniform_inputs(oracle, ring.input_sizes, 1)
-    x, y = ring.run(inputs), two.run(inputs)
+    sources = "\n".join(ring_graph.kernel_sources)
+    assert f"mc_gemm_f32_ring<{config}>" in sources, ring_graph.launch_names
+    assert ring_graph.kernel_launches == 2
+    inputs = uniform_inputs(oracle, ring_graph.input_sizes, 1)
+    x, y = ring_graph.run(inputs), two.run(inputs)
     for p, q in zip(x, y):
         assert np.array_equal(p.view(np.uint32), q.view(np.uint32))
 

@@ -26,9 +26,9 @@ def plan(mc):
 
 
 @pytest.mark.parametrize("m,n,k,depth,want", [
-    (8192, 8192, 8192, 1, (BIG, 256, 256)),      # 1024 tiles of 256x256, persistent
-    (4096, 4096, 4096, 1, (BIG, 256, 256)),
-    (8192, 2048, 512, 1, (BIG, 256, 256)),       # the MLP's GEMM1 at B=8192
+    (8192, 8192, 8192, 1, (WIDE, 512, 256)),     # 4096 tiles of 128x128, two persistent blocks per CU
+    (4096, 4096, 4096, 1, (WIDE, 512, 256)),
+    (8192, 2048, 512, 1, (WIDE, 512, 256)),      # the MLP's GEMM1 at B=8192
     (8192, 512, 2048, 1, (WIDE8, 256, 512)),     # its GEMM2: one 128x128 tile per CU
     (2048, 2048, 2048, 1, (WIDE8, 256, 512)),
     (1024, 1024, 1024, 4, (WIDE8, 256, 512)),    # 64 tiles x 4 splits

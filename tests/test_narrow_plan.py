@@ -54,3 +54,12 @@ def test_a_forced_plan_takes_any_shape_that_fits_and_refuses_the_rest(plan):
     assert plan(2048, 2048, 512, 2, force=1) is not None
     assert plan(64, 64, 40, 1, force=1) is None   # K not a multiple of 16
     assert plan(64, 66, 64, 1, force=1) is None   # N not a multiple of 4
+
+
+def test_products_past_the_buffer_offset_range_do_not_take_the_narrow_body(plan):
+    # The narrow body's buffer loads take 31-bit byte offsets from a block's
+    # origin (up to 64 rows of A, K + 16 rows of B): a B of 2 GiB or more
+    # goes to another body.
+    assert plan(16, 16384, 32768, 8) is None          # (32768 + 16) x 16384 x 4 B >= 2^31
+    assert plan(16, 16384, 32736, 8) is not None      # (32736 + 16) x 16384 x 4 B < 2^31
+    assert plan(16, 64, 8 << 20, 8) is None           # 64 rows x 8 Mi k x 4 B = 2^31

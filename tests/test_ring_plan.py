@@ -49,3 +49,25 @@ def test_a_forced_configuration_keeps_its_tiles_in_persistent_blocks(plan):
 def test_shapes_the_ring_cannot_take(plan):
     assert plan(64, 64, 40)[0] == NONE   # K not a multiple of 32
     assert plan(64, 66, 64)[0] == NONE   # N not a multiple of 4
+
+
+def test_products_past_the_buffer_offset_range_do_not_take_the_ring(plan):
+    # The ring's buffer loads take 31-bit byte offsets from a tile's origin
+    # (256 rows of A, K + 32 rows of B).
+    assert plan(64, 16384, 32768)[0] == NONE          # (32768 + 32) x 16384 x 4 B >= 2^31
+    assert plan(64, 16384, 32704)[0] != NONE          # (32704 + 32) x 16384 x 4 B < 2^31
+    assert plan(64, 64, 2 << 20)[0] == NONE           # 256 rows x 2 Mi k x 4 B = 2^31
+
+
+def test_the_bf16_fast_kernel_bounds_its_offsets(mc):
+    f = mc.library().mchip_mfma16_fast_fits
+    f.argtypes = [ctypes.c_int] * 3
+    f.restype = ctypes.c_int
+    assert f(8192, 8192, 8192) == 1
+    assert f(4096, 14336, 4096) == 1
+    assert f(64, 8, 64) == 1
+    assert f(64, 8, 96) == 0                          # K not a multiple of 64
+    assert f(64, 12, 64) == 0                         # N not a multiple of 8
+    assert f(64, 32768, 32768) == 0                   # 2 x (32768 + 32) x 32768 B >= 2^31
+    assert f(64, 32768, 32704) == 1                   # 2 x (32704 + 32) x 32768 B < 2^31
+    assert f(64, 64, 4 << 20) == 0                    # 2 x 256 rows x 4 Mi k B = 2^31

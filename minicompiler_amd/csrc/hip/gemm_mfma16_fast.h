@@ -331,6 +331,11 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
     } else {
         const int t = full + (bid - full) / 2, half = (bid - full) % 2;
         const int tm = t / tiles_n, tn = t % tiles_n;
-        fast_tile<kBf16, kFBM / 2>(lds, a, b, c, m, n, k, tm * kFBM + half * (kFBM / 2), tn * kFBN, epilogue);
+        const int row0 = tm * kFBM + half * (kFBM / 2);
+        // In a last tile row of at most 128 rows the second half has no row
+        // of C: it has nothing to store, and its clamped rows would sit
+        // before its origin (fetch offsets below zero).
+        if (row0 >= m) return;
+        fast_tile<kBf16, kFBM / 2>(lds, a, b, c, m, n, k, row0, tn * kFBN, epilogue);
     }
 }

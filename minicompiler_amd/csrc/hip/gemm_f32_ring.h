@@ -160,6 +160,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mc_ring_rsrc(const float* base
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
 }
 
+// Non-temporal buffer stores of 1, 2 or 4 floats at byte offset voffset +
+// soffset from the resource's base (plain functions, like the LDS load).
+__device__ __forceinline__ void mc_ring_buffer_store(float v, __amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voffset, soffset, 2);
+}
+typedef unsigned mc_ring_u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned mc_ring_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void mc_ring_buffer_store(mc_ring_f32x2 v, __amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(mc_ring_u32x2, v), r, voffset, soffset, 2);
+}
+__device__ __forceinline__ void mc_ring_buffer_store(mc_ring_f32x4 v, __amdgpu_buffer_rsrc_t r, int voffset, int soffset) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(mc_ring_u32x4, v), r, voffset, soffset, 2);
+}
+
 // Global -> LDS without registers: buffer_load_dwordx4 ... lds writes lane
 // l's 16 bytes at (LDS base + 16 l). (A plain function: called in a
 // template, the builtin failed the host pass of the AOT build.)
@@ -358,9 +372,19 @@ __device__ __forceinline__ void mc_ring_barrier() {
 // with device-scope stores (mc_split_store).
 template <class Cfg, bool kCheck, typename Epilogue, bool kSplit = false>
 __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::kAI][Cfg::kBJ], float* __restrict__ out,
-                                              int row0, int col, int m, int n, bool raw, const Epilogue& epilogue) {
+                                              int tile_row0, int tile_col0, int row0, int col, int m, int n, bool raw,
+                                              const Epilogue& epilogue) {
     typedef McRingVec<Cfg::kBJ> BV;
     auto row_of = [&](int i, int v) { return row0 + 32 * i + 8 * (v >> 2) + (v & 3); };
+    // Buffer stores from the tile's origin in C: the lane's byte offset in a
+    // vector register, each row's distance from the lane's first row (a
+    // multiple of 4 n) in a scalar one, so no vector instruction computes a
+    // store address (the 64-bit addresses they replace took about four
+    // vector ALU instructions per store, which a SIMD does not run beside
+    // MFMAs). The host keeps the offsets below 2^31 (256 rows of C).
+    const __amdgpu_buffer_rsrc_t c_rsrc = mc_ring_rsrc(out + static_cast<long long>(tile_row0) * n + tile_col0);
+    const int c_off = 4 * ((row0 - tile_row0) * n + (col - tile_col0));
+    auto row_step = [&](int i, int v) { return 4 * n * (32 * i + 8 * (v >> 2) + (v & 3)); };
     if constexpr (kSplit) {
 #pragma unroll
         for (int i = 0; i < Cfg::kAI; ++i)
@@ -388,7 +412,7 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
                     const float x = acc[i][j][v];
                     BV::set(o, j, raw ? x : epilogue(x, static_cast<unsigned>(at + j)));
                 }
-                __builtin_nontemporal_store(o, reinterpret_cast<typename BV::type*>(out + at));
+                mc_ring_buffer_store(o, c_rsrc, c_off, row_step(i, v));
             }
         return;
     }
@@ -421,7 +445,7 @@ __device__ __forceinline__ void mc_ring_store(const mc_ring_f32x16 (&acc)[Cfg::k
             for (int v = 0; v < 16; ++v) {
                 const int row = row_of(i0 + di, v);
                 if (kCheck && row >= m) continue;
-                __builtin_nontemporal_store(o[di][v], reinterpret_cast<typename BV::type*>(out + static_cast<long long>(row) * n + col));
+                mc_ring_buffer_store(o[di][v], c_rsrc, c_off, row_step(i0 + di, v));
             }
     }
 }
@@ -678,13 +702,13 @@ __device__ __forceinline__ void mc_gemm_f32_ring(const float* __restrict__ a, co
             const int r0 = u.row0 + wr + 4 * half;
             if (fold) {
                 if (u.row0 + Cfg::kBM <= m)
-                    mc_ring_store<Cfg, false, Epilogue, true>(acc, out, r0, col, m, n, true, epilogue);
+                    mc_ring_store<Cfg, false, Epilogue, true>(acc, out, u.row0, u.col0, r0, col, m, n, true, epilogue);
                 else
-                    mc_ring_store<Cfg, true, Epilogue, true>(acc, out, r0, col, m, n, true, epilogue);
+                    mc_ring_store<Cfg, true, Epilogue, true>(acc, out, u.row0, u.col0, r0, col, m, n, true, epilogue);
             } else if (u.row0 + Cfg::kBM <= m) {
-                mc_ring_store<Cfg, false>(acc, out, r0, col, m, n, splits > 1, epilogue);
+                mc_ring_store<Cfg, false>(acc, out, u.row0, u.col0, r0, col, m, n, splits > 1, epilogue);
             } else {
-                mc_ring_store<Cfg, true>(acc, out, r0, col, m, n, splits > 1, epilogue);
+                mc_ring_store<Cfg, true>(acc, out, u.row0, u.col0, r0, col, m, n, splits > 1, epilogue);
             }
         }
         if (fold) {

@@ -390,9 +390,13 @@ extern "C" int mchip_f32_ring_plan_cfg(int m, int n, int k, int depth, int cu_co
     if (m < 1 || n < 4 || k < kRBKRing || k % kRBKRing != 0 || n % 4 != 0 || depth < 1 || cu_count < 1) {
         return MCHIP_RING_NONE;
     }
-    // The ring's buffer loads take 31-bit byte offsets from a tile's origin:
-    // up to 256 rows of A and K + 32 rows of B past it.
-    if (256LL * k * 4 >= (1LL << 31) || (static_cast<long long>(k) + 32) * n * 4 >= (1LL << 31)) return MCHIP_RING_NONE;
+    // The ring's buffer loads and stores take 31-bit byte offsets from a
+    // tile's origin: up to 256 rows of A, K + 32 rows of B and 256 rows of C
+    // past it.
+    if (256LL * k * 4 >= (1LL << 31) || (static_cast<long long>(k) + 32) * n * 4 >= (1LL << 31) ||
+        256LL * n * 4 >= (1LL << 31)) {
+        return MCHIP_RING_NONE;
+    }
     if (cfg != MCHIP_RING_NONE) {
         // A forced configuration: its tiles, in persistent blocks (at most
         // one per CU for big, thin and wide8, two for wide and mid).

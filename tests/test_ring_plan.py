@@ -52,11 +52,13 @@ def test_shapes_the_ring_cannot_take(plan):
 
 
 def test_products_past_the_buffer_offset_range_do_not_take_the_ring(plan):
-    # The ring's buffer loads take 31-bit byte offsets from a tile's origin
-    # (256 rows of A, K + 32 rows of B).
+    # The ring's buffer loads and stores take 31-bit byte offsets from a
+    # tile's origin (256 rows of A, K + 32 rows of B, 256 rows of C).
     assert plan(64, 16384, 32768)[0] == NONE          # (32768 + 32) x 16384 x 4 B >= 2^31
     assert plan(64, 16384, 32704)[0] != NONE          # (32704 + 32) x 16384 x 4 B < 2^31
     assert plan(64, 64, 2 << 20)[0] == NONE           # 256 rows x 2 Mi k x 4 B = 2^31
+    assert plan(64, 2 << 20, 32)[0] == NONE           # 256 rows of C x 2 Mi n x 4 B = 2^31
+    assert plan(64, (2 << 20) - 4, 32)[0] != NONE     # one column chunk fewer
 
 
 def test_the_bf16_fast_kernel_bounds_its_offsets(mc):

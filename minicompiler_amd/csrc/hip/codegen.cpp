@@ -97,10 +97,21 @@ const char* const kOnePlusTanhSource = R"(__device__ __forceinline__ float mc_on
 
 )";
 
+// (1 + tanh(x)) / 2 = 1 / (1 + e^{-2x}): the same exp2 and reciprocal as
+// mc_one_plus_tanh, without its doubling.
+const char* const kHalfOnePlusTanhSource = R"(__device__ __forceinline__ float mc_half_one_plus_tanh(float x)
+{
+	const float e = __builtin_amdgcn_exp2f(x * __uint_as_float(0xc038aa3bu) /* -2 log2(e) */);
+	return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+)";
+
 // How each instruction of a program is emitted.
 struct Form {
-    enum class Kind : std::uint8_t { Plain, Absorbed, OnePlusTanh, Fma } kind = Kind::Plain;
-    // OnePlusTanh: x = tanh's operand. Fma: x * y + z (with `neg_x`: -x * y + z, `neg_z`: x * y - z).
+    enum class Kind : std::uint8_t { Plain, Absorbed, OnePlusTanh, HalfOnePlusTanh, Fma } kind = Kind::Plain;
+    // OnePlusTanh: x = tanh's operand. HalfOnePlusTanh: x * mc_half_one_plus_tanh(y).
+    // Fma: x * y + z (with `neg_x`: -x * y + z, `neg_z`: x * y - z).
     std::int32_t x = -1, y = -1, z = -1;
     bool neg_x = false, neg_z = false;
 };
@@ -109,6 +120,10 @@ struct Form {
 // as it is, so it rounds exactly as the reference's op does):
 // - an add of the immediate 1.0 and a tanh used only there becomes
 //   mc_one_plus_tanh of the tanh's operand;
+// - a mul of such a sum (used only there) by x * 0.5 (used only there), the
+//   tail of GELU, becomes x * mc_half_one_plus_tanh: (x / 2)(2 r) is x r
+//   exactly wherever x / 2 is exact (all but |x| < 2^-125), two multiplies
+//   fewer per element;
 // - a mul used only by one add or sub becomes an fmaf there (one rounding
 //   instead of two), as NVRTC contracts a*b+c by default: the reference's
 //   run-time compile passes no option against it (src/cuda/kernel_compiler.cpp:35-37).
@@ -160,6 +175,26 @@ std::vector<Form> program_forms(const FusedProgram& program) {
             }
         }
     }
+    // (x * 0.5) * (1 + tanh u), each factor used only there.
+    auto is_half = [&](std::int32_t r) {
+        const FusedInstr& i = program.instrs[r];
+        return i.kind == FusedInstr::Kind::Immediate && i.immediate == 0.5f;
+    };
+    for (std::size_t r = 0; r < n; ++r) {
+        const FusedInstr& ins = program.instrs[r];
+        if (ins.kind != FusedInstr::Kind::Binary || ins.op != OpKind::Mul || forms[r].kind != Form::Kind::Plain) continue;
+        for (const auto& [p, h] : {std::pair{ins.a, ins.b}, std::pair{ins.b, ins.a}}) {
+            if (p == h || forms[p].kind != Form::Kind::OnePlusTanh || uses[p] != 1) continue;
+            if (!is(h, OpKind::Mul, FusedInstr::Kind::Binary)) continue;
+            const FusedInstr& hm = program.instrs[h];
+            const std::int32_t x = is_half(hm.b) ? hm.a : is_half(hm.a) ? hm.b : -1;
+            if (x < 0) continue;
+            forms[r] = {Form::Kind::HalfOnePlusTanh, x, forms[p].x};
+            forms[p].kind = Form::Kind::Absorbed;
+            forms[h].kind = Form::Kind::Absorbed;
+            break;
+        }
+    }
     return forms;
 }
 
@@ -169,7 +204,7 @@ std::vector<Form> program_forms(const FusedProgram& program) {
 // fuses two instructions into one.
 std::string program_function(const FusedProgram& program, std::size_t num_inputs) {
     const std::vector<Form> forms = program_forms(program);
-    bool tanh = false, one_plus_tanh = false;
+    bool tanh = false, one_plus_tanh = false, half_one_plus_tanh = false;
     std::ostringstream body;
     auto reg = [](std::int32_t r) { return "r" + std::to_string(r); };
     for (std::size_t r = 0; r < program.instrs.size(); ++r) {
@@ -180,6 +215,9 @@ std::string program_function(const FusedProgram& program, std::size_t num_inputs
         if (f.kind == Form::Kind::OnePlusTanh) {
             one_plus_tanh = true;
             body << "mc_one_plus_tanh(" << reg(f.x) << ")";
+        } else if (f.kind == Form::Kind::HalfOnePlusTanh) {
+            half_one_plus_tanh = true;
+            body << reg(f.x) << " * mc_half_one_plus_tanh(" << reg(f.y) << ")";
         } else if (f.kind == Form::Kind::Fma) {
             body << "fmaf(" << (f.neg_x ? "-" : "") << reg(f.x) << ", " << reg(f.y) << ", " << (f.neg_z ? "-" : "")
                  << reg(f.z) << ")";
@@ -199,6 +237,7 @@ std::string program_function(const FusedProgram& program, std::size_t num_inputs
     std::ostringstream os;
     if (tanh) os << kTanhSource;
     if (one_plus_tanh) os << kOnePlusTanhSource;
+    if (half_one_plus_tanh) os << kHalfOnePlusTanhSource;
     os << "__device__ __forceinline__ float mc_program(";
     for (std::size_t k = 0; k < num_inputs; ++k) os << (k ? ", " : "") << "float x" << k;
     if (num_inputs == 0) os << "void";

@@ -37,9 +37,9 @@ def test_fused_gelu_is_one_vectorised_kernel(mc):
     # Exact bit patterns, once, in the program (before the kernel's loop).
     assert src.count("__uint_as_float(0x3f000000u)") == 1
     assert src.index("0x3f000000u") < kernel_loop(src)
-    # 1 + tanh(u) is one mc_one_plus_tanh, x + x^3 coef one fmaf, in the program ...
-    assert src.count("mc_one_plus_tanh(r") == 1 and "mc_tanh" not in src
-    assert src.count("float mc_one_plus_tanh(float x)") == 1  # (defined once)
+    # (x / 2)(1 + tanh u) is x times one mc_half_one_plus_tanh, x + x^3 coef one fmaf, in the program ...
+    assert "r0 * mc_half_one_plus_tanh(r7)" in src and "mc_tanh" not in src and "mc_one_plus_tanh" not in src
+    assert src.count("float mc_half_one_plus_tanh(float x)") == 1  # (defined once)
     assert src.count("fmaf(") == 1
     assert src.count("mc_program(a0[u].") == 8     # ... applied to 4 lanes, full and ragged steps
 
@@ -63,6 +63,14 @@ def test_multi_op_programs_contract_a_mul_used_once_into_its_add_or_sub(mc):
     assert "fmaf" not in program_of(src)
     src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = load in1\nr2 = mul r0, r1\n", shapes[:2], (64,))
     assert "fmaf" not in program_of(src) and "const float r2 = r0 * r1;" in src
+    # 1 + tanh u alone (not halved), or halved by a product used twice: mc_one_plus_tanh, the multiplies kept.
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = imm 1.0\nr2 = tanh r0\nr3 = add r2, r1\n"
+                                            "r4 = mul r0, r3\n", shapes[:1], (64,))
+    assert "const float r3 = mc_one_plus_tanh(r0);" in program_of(src) and "mc_half" not in src
+    src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = imm 1.0\nr2 = tanh r0\nr3 = add r2, r1\n"
+                                            "r4 = imm 0.5\nr5 = mul r0, r4\nr6 = mul r5, r3\nr7 = div r6, r5\n",
+                                            shapes[:1], (64,))
+    assert "mc_half" not in src and "const float r6 = r5 * r3;" in program_of(src)
     # tanh plus an immediate other than 1, or a tanh used twice: the plain tanh.
     src, _ = mc.generate_elementwise_kernel("r0 = load in0\nr1 = imm 2.0\nr2 = tanh r0\nr3 = add r2, r1\n",
                                             shapes[:1], (64,))

@@ -108,6 +108,40 @@ def test_one_plus_tanh_in_a_fused_group_over_a_dense_range(device, mc):
     assert np.all(np.isnan(nan.run([np.full(4, np.nan, np.float32)])[0]))
 
 
+def test_halved_one_plus_tanh_equals_the_unhalved_form_bit_for_bit(device, mc):
+    # GELU's tail (x * 0.5)(1 + tanh u) is emitted as x * mc_half_one_plus_tanh(u)
+    # = x / (1 + 2^(-2 u log2 e)): the same bits as (x / 2) times the
+    # mc_one_plus_tanh form wherever x / 2 is exact. The second graph also
+    # outputs x * 0.5, which puts it in a kernel of its own, so its group
+    # multiplies the loaded half by mc_one_plus_tanh.
+    xs = np.concatenate([np.linspace(-60, 60, 96001, dtype=np.float32),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 1e30, -1e30, np.inf, -np.inf, np.nan], np.float32)])
+    head = f"input x : f32[{xs.size}]\nconst one : f32[] = 1.0\nconst half : f32[] = 0.5\n"
+    body = "t = tanh x\np = add t, one\nh = mul x, half\ny = mul h, p\noutput y\n"
+    fused = mc.Compiled(head + body)
+    assert any("mc_half_one_plus_tanh(" in s for s in fused.kernel_sources)
+    split = mc.Compiled(head + body + "output h\n")
+    assert not any("mc_half_one_plus_tanh(" in s for s in split.kernel_sources)
+    assert any("mc_one_plus_tanh(" in s for s in split.kernel_sources)
+    a = fused.run([xs])[0]
+    b = split.run([xs])[0]
+    nan = np.isnan(a)
+    assert np.array_equal(nan, np.isnan(b))
+    assert np.array_equal(a[~nan].view(np.uint32), b[~nan].view(np.uint32))
+    # And against float64: x / (1 + e^(-2x)), within the bound of the form
+    # above, plus 6e-37 absolute: the reciprocal returns 0 where it would be
+    # below the smallest normal float (for x below about -43.67), so the form
+    # returns -0 where the exact value is below 5.2e-37 in magnitude.
+    x64 = xs.astype(np.float64)
+    fin = np.isfinite(x64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = x64 / (1.0 + np.exp(-2.0 * x64))
+    bound = (5 * 2.0**-24 + 2 * np.abs(np.where(fin, x64, 0.0)) * 2.0 * np.log2(np.e) * 2.0**-24 * np.log(2)) \
+        * np.abs(np.where(fin, ref, 0.0)) + 6e-37
+    bad = fin & (np.abs(a.astype(np.float64) - np.where(fin, ref, 0.0)) > bound)
+    assert not np.any(bad), (xs[bad][:5], a[bad][:5], ref[bad][:5])
+
+
 @pytest.mark.parametrize("sa,sb", PATTERNS)
 def test_binary_ops_match_bit_for_bit_for_every_broadcast_pattern(device, mc, oracle, sa, sb):
     for op in BINARY:

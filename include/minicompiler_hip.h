@@ -219,6 +219,24 @@ MC_API int mc_launch_matmul_lowp(int kernel, int dtype, const void* a, const voi
                                  void* stream, int splits, float* workspace);
 /* fp32 to bf16 (dtype 1) / fp16 (dtype 2), round to nearest even. */
 MC_API int mc_convert_f32(int dtype, const float* in, void* out, size_t count, void* stream);
+/* Packed A for the bf16/fp16 kernel. No counterpart in the reference, whose
+ * tensor-core kernel (matmul_tensor_core.cu:96-297) stages row-major fp32.
+ * A is cut into 256-row bands (the last padded with zero rows) and each band
+ * into 32-k steps, each (band, step) block 16 KiB in the kernel's LDS order:
+ * element (row, kk) at index (row / 256) 256 k + (kk / 32) 8192 +
+ * (row % 256 / 16) 512 + (kk % 32 / 8) 128 + (row % 16) 8 + kk % 8.
+ * mc_packed_a16_bytes: its size for an m x k operand; mc_pack_a16: 16-bit
+ * row-major A packed; mc_convert_pack_a_f32: fp32 A rounded to bf16 (dtype 1)
+ * / fp16 (dtype 2) as mc_convert_f32 rounds and packed (k a multiple of 64,
+ * pointers 16-byte aligned); mc_launch_matmul_lowp_packed: the product on
+ * packed A and row-major B (K a multiple of 64, N of 8, 16-byte aligned
+ * pointers, else hipErrorInvalidValue), the same bits as mc_launch_matmul_lowp
+ * on row-major A. Compiled graphs pack the operands they round. */
+MC_API long long mc_packed_a16_bytes(int m, int k);
+MC_API int mc_pack_a16(const void* a, void* packed, int m, int k, void* stream);
+MC_API int mc_convert_pack_a_f32(int dtype, const float* a, void* packed, int m, int k, void* stream);
+MC_API int mc_launch_matmul_lowp_packed(int kernel, int dtype, const void* a_packed, const void* b, float* c, int m,
+                                        int n, int k, void* stream);
 /* c = sum of `splits` partials of `count` floats, fixed order (matmul_kernels.hpp:53-59). */
 MC_API int mc_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
 MC_API int mc_split_k_splits(int m, int n, int k, int cu_count, int blocks_per_cu); /* matmul_kernels.hpp:11-17 */

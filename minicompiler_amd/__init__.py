@@ -105,6 +105,10 @@ _SIGNATURES = {
     "mc_launch_matmul_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _vp, _i]),
     "mc_noalloc_scratch_bytes": (_c.c_ulonglong, []),
     "mc_convert_f32": (_i, [_i, _vp, _vp, _sz, _vp]),
+    "mc_packed_a16_bytes": (_ll, [_i, _i]),
+    "mc_pack_a16": (_i, [_vp, _vp, _i, _i, _vp]),
+    "mc_convert_pack_a_f32": (_i, [_i, _vp, _vp, _i, _i, _vp]),
+    "mc_launch_matmul_lowp_packed": (_i, [_i, _i, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "mc_sum_split_partials": (_i, [_vp, _vp, _sz, _i, _vp]),
     "mc_split_k_splits": (_i, [_i, _i, _i, _i, _i]),
     "mc_matmul_splits": (_i, [_i, _i, _i, _i, _i]),
@@ -629,6 +633,29 @@ def memcpy_dtod_async(dst: int, src: int, nbytes: int, stream=None) -> None:
 
 def convert_f32(dtype: int, src: int, dst: int, count: int, stream=None) -> None:
     _check(library().mc_convert_f32(dtype, src, dst, count, _stream_handle(stream)), "convert_f32")
+
+
+def packed_a16_bytes(m: int, k: int) -> int:
+    """Bytes of packed A (mc_pack_a16's layout) for an m x k operand."""
+    return int(library().mc_packed_a16_bytes(m, k))
+
+
+def pack_a16(src: int, dst: int, m: int, k: int, stream=None) -> None:
+    """16-bit row-major A [m, k] to packed A."""
+    _check(library().mc_pack_a16(src, dst, m, k, _stream_handle(stream)), "pack_a16")
+
+
+def convert_pack_a_f32(dtype: int, src: int, dst: int, m: int, k: int, stream=None) -> None:
+    """fp32 row-major A [m, k] rounded to bf16 (dtype 1) / fp16 (dtype 2) and packed."""
+    _check(library().mc_convert_pack_a_f32(dtype, src, dst, m, k, _stream_handle(stream)), "convert_pack_a_f32")
+
+
+def launch_matmul_lowp_packed(kernel: int | str, dtype: int, a_packed: int, b: int, c: int, m: int, n: int, k: int,
+                              stream=None) -> None:
+    """The bf16/fp16 product on packed A and row-major 16-bit B."""
+    kid = matmul_kernel_id(kernel) if isinstance(kernel, str) else kernel
+    _check(library().mc_launch_matmul_lowp_packed(kid, dtype, a_packed, b, c, m, n, k, _stream_handle(stream)),
+           f"launch_matmul_lowp_packed({matmul_kernel_name(kid)})")
 
 
 def sum_split_partials(partial: int, c: int, count: int, splits: int, stream=None) -> None:

@@ -849,6 +849,21 @@ MC_API int mc_convert_f32(int dtype, const float* in, void* out, size_t count, v
     return mchip_convert_f32(dtype, in, out, count, stream);
 }
 
+MC_API long long mc_packed_a16_bytes(int m, int k) { return 2 * mchip_packed_a16_elements(m, k); }
+
+MC_API int mc_pack_a16(const void* a, void* packed, int m, int k, void* stream) {
+    return mchip_pack_a16(a, packed, m, k, stream);
+}
+
+MC_API int mc_convert_pack_a_f32(int dtype, const float* a, void* packed, int m, int k, void* stream) {
+    return mchip_convert_pack_a_f32(dtype, a, packed, m, k, stream);
+}
+
+MC_API int mc_launch_matmul_lowp_packed(int kernel, int dtype, const void* a_packed, const void* b, float* c, int m,
+                                        int n, int k, void* stream) {
+    return mchip_launch_matmul_lowp_packed(kernel, dtype, a_packed, b, c, m, n, k, stream);
+}
+
 MC_API int mc_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream) {
     return mchip_sum_split_partials(partial, c, count, splits, stream);
 }

@@ -334,11 +334,12 @@ GemmEpilogueKernel generate_gemm_epilogue_kernel(const FusedProgram& program, st
                                        : std::string("k_split, depth");
     const char* unused = constant ? "\t(void)m;\n\t(void)n;\n\t(void)k;\n" : "";
     if (!is_f32_body(body)) {
+        // `a` is packed A (the graph rounds and packs it, mc_convert_pack_a_f32).
         os << "extern \"C\" __global__ void __launch_bounds__(512, 1)\n" << kGemmEpilogueKernelName
            << "(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b, float* __restrict__ c, "
               "int m, int n, int k, McEpilogue epi)\n{\n"
            << unused << "\tmc_gemm16_fast<" << (body == GemmBody::Bf16Fast ? "true" : "false")
-           << ">(a, b, c, " << mnk << ", epi);\n}\n";
+           << ", true>(a, b, c, " << mnk << ", epi);\n}\n";
         return {os.str()};
     }
     const char* bounds = body == GemmBody::F32RingBig || body == GemmBody::F32RingThin ? "256, 1"

@@ -80,6 +80,21 @@ struct McGemm16Store {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
+// Packed A (the kPackedA form; mc_pack_a16 and the compiled graphs' rounding
+// of fp32 operands write it): A cut into bands of 256 rows (the last band
+// padded with zero rows) and each band into K steps of 32, every (band, step)
+// block 16 KiB in the order of a stage's A region, so that each fetch
+// instruction reads 1 KiB linearly instead of 64 bytes from each of 16 rows.
+// Element (row, kk) of an M x K matrix sits at index
+//   (row / 256) 256 K + (kk / 32) 8192 + (row % 256 / 16) 512 + (kk % 32 / 8) 128 + (row % 16) 8 + kk % 8.
+// On an MI355X the 8192^3 bf16 product took 787-795 us so against 840-845 us
+// with row-major A (timing copies, one process); the same layout for B
+// gained nothing (B's fetch already reads 512 bytes per k row).
+__device__ __forceinline__ long long mc_packed_a16_index(int row, int kk, int k) {
+    return static_cast<long long>(row >> 8) * 256 * k + static_cast<long long>(kk >> 5) * 8192 +
+           ((row & 255) >> 4) * 512 + ((kk & 31) >> 3) * 128 + (row & 15) * 8 + (kk & 7);
+}
+
 __device__ __forceinline__ int mc_min16(int a, int b) { return a < b ? a : b; }
 #define MC_LDS __attribute__((address_space(3)))
 
@@ -115,6 +130,7 @@ template <int kRows>
 struct FastLane {
     __amdgpu_buffer_rsrc_t a_rsrc, b_rsrc;
     int a_src[FastShape<kRows>::kFetchA];  // byte offset of the A chunk this lane fetches per instruction (k 0)
+    int a_step;                            // bytes between consecutive K steps of A (64 row-major, 16 KiB packed)
     int b_src[2];                          // byte offset of the B chunk (k row 0)
     int b_step;                            // bytes between consecutive K steps of B
     int a_off[FastShape<kRows>::kRowFrags];  // LDS byte offsets of the A fragments
@@ -136,7 +152,7 @@ __device__ __forceinline__ void fast_fetch(MC_LDS unsigned char* wr, const FastL
     MC_LDS unsigned char* sa = wr + L.wave * kFA * 1024;
     MC_LDS unsigned char* sb = wr + kFBOffset + L.wave * 4 * 512;
 #pragma unroll
-    for (int i = 0; i < kFA; ++i) fast_buffer_to_lds(L.a_rsrc, sa + i * 1024, L.a_src[i], 2 * fetch_k);
+    for (int i = 0; i < kFA; ++i) fast_buffer_to_lds(L.a_rsrc, sa + i * 1024, L.a_src[i], (fetch_k / kFBK) * L.a_step);
     const int bk = (fetch_k / kFBK) * L.b_step;
 #pragma unroll
     for (int i = 0; i < 2; ++i) fast_buffer_to_lds(L.b_rsrc, sb + i * 1024, L.b_src[i], bk);
@@ -212,7 +228,7 @@ __device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kRowFrags][kF
 }
 
 // One kRows x 256 tile of C at (row0, col0), all of K.
-template <bool kBf16, int kRows, typename Epilogue>
+template <bool kBf16, int kRows, bool kPackedA, typename Epilogue>
 __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsigned short* __restrict__ a,
                                           const unsigned short* __restrict__ b, float* __restrict__ c, int m, int n,
                                           int k, int row0, int col0, const Epilogue& epilogue) {
@@ -222,17 +238,27 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
 
     FastLane<kRows> L;
     L.wave = wave;
-    L.a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(a) + static_cast<long long>(row0) * k, 0,
-                                                 0x7fffffff, 0x00020000);
+    // Row-major A: based at row row0. Packed A: at the row's 256-row band,
+    // plus 8 KiB for the second half of a band, the step blocks 16 KiB apart.
+    const long long a_base = kPackedA ? static_cast<long long>(row0 / kFBM) * k * kFBM + (row0 % kFBM) * 32
+                                      : static_cast<long long>(row0) * k;
+    L.a_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(a) + a_base, 0, 0x7fffffff, 0x00020000);
+    L.a_step = kPackedA ? kFBM * kFBK * 2 : kFBK * 2;
     L.b_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(b) + col0, 0, 0x7fffffff, 0x00020000);
     // A: wave w fills the 16-row blocks kFetchA w + i, one per instruction;
     // lane -> (row 16 (kFetchA w + i) + l % 16, chunk l / 16). Rows past the
     // edge are clamped, so every offset is at or past the origin.
 #pragma unroll
     for (int i = 0; i < Sh::kFetchA; ++i) {
-        const int r = (wave * Sh::kFetchA + i) * 16 + (lane & 15);
-        const int gr = mc_min16(row0 + r, m - 1);
-        L.a_src[i] = 2 * ((gr - row0) * k + (lane >> 4) * 8);
+        if constexpr (kPackedA) {
+            // The stage's A bytes as they lie in a step block: 1 KiB per
+            // instruction, read linearly.
+            L.a_src[i] = (wave * Sh::kFetchA + i) * 1024 + lane * 16;
+        } else {
+            const int r = (wave * Sh::kFetchA + i) * 16 + (lane & 15);
+            const int gr = mc_min16(row0 + r, m - 1);
+            L.a_src[i] = 2 * ((gr - row0) * k + (lane >> 4) * 8);
+        }
     }
     // B: wave w fills k rows 4 w .. 4 w + 3, two per instruction; lane ->
     // (k row 4 w + 2 i + l / 32, physical chunk l % 32).
@@ -314,7 +340,7 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
 // per block on all of them (mchip_mfma16_fast_grid picks the count). Every C
 // element gets the same MFMA sequence either way, so the results are the
 // same bits.
-template <bool kBf16, typename Epilogue>
+template <bool kBf16, bool kPackedA, typename Epilogue>
 __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict__ a, const unsigned short* __restrict__ b,
                                                float* __restrict__ c, int m, int n, int k, const Epilogue& epilogue) {
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kFStages * kFStage];
@@ -327,7 +353,7 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
     const int bid = static_cast<int>(blockIdx.x);
     if (bid < full) {
         const int tm = bid / tiles_n, tn = bid % tiles_n;
-        fast_tile<kBf16, kFBM>(lds, a, b, c, m, n, k, tm * kFBM, tn * kFBN, epilogue);
+        fast_tile<kBf16, kFBM, kPackedA>(lds, a, b, c, m, n, k, tm * kFBM, tn * kFBN, epilogue);
     } else {
         const int t = full + (bid - full) / 2, half = (bid - full) % 2;
         const int tm = t / tiles_n, tn = t % tiles_n;
@@ -336,6 +362,6 @@ __device__ __forceinline__ void mc_gemm16_fast(const unsigned short* __restrict_
         // of C: it has nothing to store, and its clamped rows would sit
         // before its origin (fetch offsets below zero).
         if (row0 >= m) return;
-        fast_tile<kBf16, kFBM / 2>(lds, a, b, c, m, n, k, row0, tn * kFBN, epilogue);
+        fast_tile<kBf16, kFBM / 2, kPackedA>(lds, a, b, c, m, n, k, row0, tn * kFBN, epilogue);
     }
 }

@@ -35,6 +35,12 @@ constexpr std::size_t kArenaAlign = 256;
 
 std::size_t align_up(std::size_t v) { return (v + kArenaAlign - 1) / kArenaAlign * kArenaAlign; }
 
+// Bytes of a converted tensor-core matmul's packed A (its workspace's first part).
+template <class L>
+std::size_t packed_a_bytes(const L& l) {
+    return align_up(static_cast<std::size_t>(mchip_packed_a16_elements(l.m, l.k)) * 2);
+}
+
 Status hip_status(int rc, const char* call) {
     if (rc == 0) return Status();
     return Error{std::string(call) + ": " + mchip_error_string(rc)};
@@ -94,7 +100,8 @@ struct Launch {
     std::vector<void*> sum_params;
     // Tensor-core matmul on fp32 operands rounded to 16 bits in the launch's
     // workspace (a16, b16) first: per run, or once at compile time for a
-    // constant operand.
+    // constant operand. a16 holds A packed (mchip_convert_pack_a_f32: 256-row
+    // bands of 16 KiB K-step blocks in the kernel's LDS order), b16 B row-major.
     bool lowp = false;
     int dtype = 0;
     void* a16 = nullptr;
@@ -188,7 +195,7 @@ public:
                     l.body = fused_body(l);
                 }
                 const std::size_t ws =
-                    l.lowp ? align_up(static_cast<std::size_t>(l.m) * l.k * 2) + align_up(static_cast<std::size_t>(l.k) * l.n * 2)
+                    l.lowp ? packed_a_bytes(l) + align_up(static_cast<std::size_t>(l.k) * l.n * 2)
                            : matmul_workspace_bytes(l.matmul, l.m, l.n, l.splits);
                 workspace_offset.push_back(ws ? top : SIZE_MAX);
                 if (ws) top += align_up(ws);
@@ -212,7 +219,7 @@ public:
             Launch& l = launches_[j];
             if (l.lowp) {
                 l.a16 = base + workspace_offset[j];
-                l.b16 = base + workspace_offset[j] + align_up(static_cast<std::size_t>(l.m) * l.k * 2);
+                l.b16 = base + workspace_offset[j] + packed_a_bytes(l);
             } else {
                 l.workspace = reinterpret_cast<float*>(base + workspace_offset[j]);
             }
@@ -232,8 +239,8 @@ public:
         for (const Launch& l : launches_) {
             if (!l.lowp) continue;
             if (!l.convert_a) {
-                MCHIP_TRY(mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16,
-                                            static_cast<std::size_t>(l.m) * l.k, stream_));
+                MCHIP_TRY(mchip_convert_pack_a_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16, l.m,
+                                                   l.k, stream_));
             }
             if (!l.convert_b) {
                 MCHIP_TRY(mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(b_of(l))), l.b16,
@@ -484,8 +491,8 @@ private:
         if (l.lowp) {
             int rc = 0;
             if (l.convert_a) {
-                rc = mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16,
-                                       static_cast<std::size_t>(l.m) * l.k, s);
+                rc = mchip_convert_pack_a_f32(l.dtype, static_cast<const float*>(value_ptr(a_of(l))), l.a16, l.m, l.k,
+                                              s);
             }
             if (rc == 0 && l.convert_b) {
                 rc = mchip_convert_f32(l.dtype, static_cast<const float*>(value_ptr(b_of(l))), l.b16,
@@ -496,10 +503,10 @@ private:
                 rc = mchip_module_launch(l.function, l.grid_x, 512, 0, s, l.params.data());
                 return rc == 0 ? Status() : hip_status(rc, "hipModuleLaunchKernel(mc_gemm_epilogue)");
             }
-            rc = mchip_launch_matmul_lowp(static_cast<int>(l.matmul), l.dtype, l.a16, l.b16,
-                                          static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s, 1, nullptr);
+            rc = mchip_launch_matmul_lowp_packed(static_cast<int>(l.matmul), l.dtype, l.a16, l.b16,
+                                                 static_cast<float*>(value_ptr(l.node)), l.m, l.n, l.k, s);
             if (rc != 0) {
-                return Error{std::string("launch_matmul_lowp(") + matmul_kernel_name(l.matmul) + "): " +
+                return Error{std::string("launch_matmul_lowp_packed(") + matmul_kernel_name(l.matmul) + "): " +
                              mchip_error_string(rc)};
             }
             return Status();

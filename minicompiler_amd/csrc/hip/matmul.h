@@ -27,6 +27,17 @@ int mchip_launch_matmul(int kernel, const float* a, const float* b, float* c, in
 int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, const void* b, float* c, int m, int n, int k,
                              void* stream, int splits, float* workspace);
 
+/* Packed A for the bf16/fp16 256x256-tile kernel (gemm_mfma16_fast.h): the
+ * elements it holds for an m x k operand (m rounded up to 256 rows), 16-bit
+ * row-major A packed, fp32 A rounded and packed in one pass (k a multiple
+ * of 64, pointers 16-byte aligned), and the product on packed A (the shapes
+ * and alignment of the fast kernel; same bits as on row-major A). */
+long long mchip_packed_a16_elements(int m, int k);
+int mchip_pack_a16(const void* a, void* packed, int m, int k, void* stream);
+int mchip_convert_pack_a_f32(int dtype, const float* a, void* packed, int m, int k, void* stream);
+int mchip_launch_matmul_lowp_packed(int kernel, int dtype, const void* a_packed, const void* b, float* c, int m, int n,
+                                    int k, void* stream);
+
 /* C = sum over z of partial[z * count + i], added in z order. */
 int mchip_sum_split_partials(const float* partial, float* c, size_t count, int splits, void* stream);
 

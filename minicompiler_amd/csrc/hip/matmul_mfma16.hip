@@ -207,11 +207,11 @@ __global__ void __launch_bounds__(256, 2) matmul_mfma16(const void* __restrict__
 // The body lives in gemm_mfma16_fast.h (also compiled at run time with fused
 // epilogues); here it is instantiated with the identity epilogue.
 
-template <bool kBf16>
+template <bool kBf16, bool kPackedA>
 __global__ void __launch_bounds__(kFThreads, 1) matmul_mfma16_fast(const unsigned short* __restrict__ a,
                                                                    const unsigned short* __restrict__ b,
                                                                    float* __restrict__ c, int m, int n, int k) {
-    mc_gemm16_fast<kBf16>(a, b, c, m, n, k, McGemm16Store{});
+    mc_gemm16_fast<kBf16, kPackedA>(a, b, c, m, n, k, McGemm16Store{});
 }
 
 // The fast path takes 16-bit A and B with K a multiple of 64, N a multiple
@@ -237,14 +237,140 @@ int device_cus() {
     return cus;
 }
 
-template <bool kBf16>
+template <bool kBf16, bool kPackedA = false>
 int launch_fast(const void* a, const void* b, float* c, int m, int n, int k, hipStream_t stream) {
     const long long tiles = static_cast<long long>((m + kFBM - 1) / kFBM) * ((n + kFBN - 1) / kFBN);
     if (tiles > 0x3fffffffLL) return hipErrorInvalidValue;
     const unsigned grid = mchip_mfma16_fast_grid(m, n, device_cus());
-    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16>), dim3(grid), dim3(kFThreads), 0, stream,
+    hipLaunchKernelGGL((matmul_mfma16_fast<kBf16, kPackedA>), dim3(grid), dim3(kFThreads), 0, stream,
                        static_cast<const unsigned short*>(a), static_cast<const unsigned short*>(b), c, m, n, k);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------ packed A
+//
+// One lane per 16-byte chunk of the packed layout (mc_packed_a16_index): 8
+// consecutive k of one row. Consecutive lanes take consecutive chunks, so a
+// wave writes 1 KiB of consecutive memory and reads 16 rows x 4 chunks
+// (64 bytes of 16-bit A, 128 of fp32 A, per row). Rows past M are zeros.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+struct PackedChunk {
+    int row, kk;
+};
+
+__device__ __forceinline__ PackedChunk packed_chunk(long long q, int steps) {
+    const long long blk = q >> 10;
+    const int w = static_cast<int>(q & 1023);
+    const int band = static_cast<int>(blk / steps), step = static_cast<int>(blk % steps);
+    return {band * kFBM + (w >> 6) * 16 + (w & 15), step * kFBK + ((w >> 4) & 3) * 8};
+}
+
+// kVec: `in` 16-byte aligned (one 16-byte load per chunk), else 8 loads of
+// 2 bytes.
+template <bool kVec>
+__global__ void __launch_bounds__(256) pack_a16_kernel(const unsigned short* __restrict__ in, u32x4* __restrict__ out,
+                                                       int m, int k, long long chunks) {
+    const int steps = k / kFBK;
+    const long long stride = static_cast<long long>(gridDim.x) * 256;
+    for (long long q = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; q < chunks; q += stride) {
+        const PackedChunk p = packed_chunk(q, steps);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (p.row < m) {
+            const unsigned short* src = in + static_cast<long long>(p.row) * k + p.kk;
+            if constexpr (kVec) {
+                v = *reinterpret_cast<const u32x4*>(src);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = src[2 * j] | (static_cast<unsigned>(src[2 * j + 1]) << 16);
+            }
+        }
+        out[q] = v;
+    }
+}
+
+// fp32 A at any 4-byte address rounded and packed, 8 loads of 4 bytes per
+// chunk. The rounding is mchip_convert_f32's.
+template <bool kBf16>
+__global__ void __launch_bounds__(256) convert_pack_a_kernel(const float* __restrict__ in, u32x4* __restrict__ out,
+                                                             int m, int k, long long chunks) {
+    const int steps = k / kFBK;
+    const long long stride = static_cast<long long>(gridDim.x) * 256;
+    for (long long q = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; q < chunks; q += stride) {
+        const PackedChunk p = packed_chunk(q, steps);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (p.row < m) {
+            const float* src = in + static_cast<long long>(p.row) * k + p.kk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                v[j] = to_bits<kBf16>(src[2 * j]) | (static_cast<unsigned>(to_bits<kBf16>(src[2 * j + 1])) << 16);
+        }
+        out[q] = v;
+    }
+}
+
+// fp32 A rounded and packed through LDS, for 16-byte aligned A: a block
+// takes kSteps K steps of one 256-row band. It reads them as rows of
+// kSteps x 128 contiguous bytes (a wave reads 1 KiB: 2 or 4 rows), writes the
+// rounded values into the band's packed blocks in LDS, then writes those out
+// as 1 KiB per wave instruction. (Reading straight into packed order, a wave
+// read 64 bytes from each of 16 rows: 4.4 TB/s on an MI355X against 6.0 for
+// the plain rounding.) In LDS each 16-byte chunk's row slot is XORed with
+// (step, chunk) % 16, which spreads a wave's 8-byte writes over the banks
+// (unswizzled, all of a row's 32 writes fall in 2 of the 64 banks); the
+// read-out undoes it, 16 lanes reading 256 contiguous bytes.
+template <bool kBf16, int kSteps>
+__global__ void __launch_bounds__(256) convert_pack_a_lds(const f32x4* __restrict__ in, u32x4* __restrict__ out, int m,
+                                                          int k, long long regions) {
+    __shared__ u32x4 tile[kSteps * 1024];
+    unsigned char* lds = reinterpret_cast<unsigned char*>(tile);
+    constexpr int kF4PerRow = kSteps * 8;
+    const int steps = k / kFBK;
+    const int per_band = steps / kSteps;
+    const int tid = static_cast<int>(threadIdx.x);
+    for (long long reg = blockIdx.x; reg < regions; reg += gridDim.x) {
+        const int band = static_cast<int>(reg / per_band), s0 = static_cast<int>(reg % per_band) * kSteps;
+        // Eight 16-byte loads in flight per lane, then their LDS writes.
+        for (int i0 = 0; i0 < kF4PerRow; i0 += 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int f = (i0 + j) * 256 + tid;
+                const int grow = band * kFBM + f / kF4PerRow;
+                v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (grow < m) {
+                    v[j] = __builtin_nontemporal_load(in + (static_cast<long long>(grow) * k + s0 * kFBK) / 4 +
+                                                      f % kF4PerRow);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int f = (i0 + j) * 256 + tid;
+                const int row = f / kF4PerRow, k4 = f % kF4PerRow;
+                const int sl = k4 >> 3, c = (k4 >> 1) & 3, eh = k4 & 1;
+                const int slot = (row & 15) ^ ((sl * 4 + c) & 15);
+                const int at = sl * 16384 + (row >> 4) * 1024 + c * 256 + slot * 16 + eh * 8;
+                typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 w = {to_bits<kBf16>(v[j][0]) | (static_cast<unsigned>(to_bits<kBf16>(v[j][1])) << 16),
+                                 to_bits<kBf16>(v[j][2]) | (static_cast<unsigned>(to_bits<kBf16>(v[j][3])) << 16)};
+                *reinterpret_cast<u32x2*>(lds + at) = w;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kSteps * 4; ++i) {
+            const int q = i * 256 + tid;
+            const int sl = q >> 10, w = q & 1023, c = (w >> 4) & 3;
+            const int slot = (w & 15) ^ ((sl * 4 + c) & 15);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(lds + sl * 16384 + (w >> 6) * 1024 + c * 256 + slot * 16);
+            out[(static_cast<long long>(band) * steps + s0 + sl) * 1024 + w] = v;
+        }
+        __syncthreads();
+    }
+}
+
+unsigned pack_blocks(long long chunks) {
+    return static_cast<unsigned>(std::max<long long>(1, std::min<long long>((chunks + 255) / 256, 16384)));
 }
 
 bool aligned(const void* p, std::uintptr_t bytes) { return reinterpret_cast<std::uintptr_t>(p) % bytes == 0; }
@@ -344,6 +470,70 @@ extern "C" int mchip_launch_matmul_lowp(int kernel, int dtype, const void* a, co
     if (kernel == kTensorCoreF16 && dtype == MCHIP_DTYPE_F16) {
         return fast ? launch_fast<false>(a, b, c, m, n, k, s) : launch16<false, false>(a, b, c, m, n, k, s, splits, workspace);
     }
+    return hipErrorInvalidValue;
+}
+
+extern "C" long long mchip_packed_a16_elements(int m, int k) {
+    if (m < 1 || k < 1) return 0;
+    return static_cast<long long>((m + kFBM - 1) / kFBM) * kFBM * k;
+}
+
+extern "C" int mchip_pack_a16(const void* a, void* packed, int m, int k, void* stream) {
+    if (m < 1 || k < 1 || k % (2 * kFBK) != 0 || !aligned(a, 2) || !aligned(packed, 16)) return hipErrorInvalidValue;
+    const long long chunks = mchip_packed_a16_elements(m, k) / 8;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* in = static_cast<const unsigned short*>(a);
+    if (aligned(a, 16)) {
+        hipLaunchKernelGGL(pack_a16_kernel<true>, dim3(pack_blocks(chunks)), dim3(256), 0, s, in,
+                           static_cast<u32x4*>(packed), m, k, chunks);
+    } else {
+        hipLaunchKernelGGL(pack_a16_kernel<false>, dim3(pack_blocks(chunks)), dim3(256), 0, s, in,
+                           static_cast<u32x4*>(packed), m, k, chunks);
+    }
+    return hipGetLastError();
+}
+
+extern "C" int mchip_convert_pack_a_f32(int dtype, const float* a, void* packed, int m, int k, void* stream) {
+    if (dtype != MCHIP_DTYPE_BF16 && dtype != MCHIP_DTYPE_F16) return hipErrorInvalidValue;
+    if (m < 1 || k < 1 || k % (2 * kFBK) != 0 || !aligned(a, 4) || !aligned(packed, 16)) return hipErrorInvalidValue;
+    const long long chunks = mchip_packed_a16_elements(m, k) / 8;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* out = static_cast<u32x4*>(packed);
+    const dim3 grid(pack_blocks(chunks));
+    const bool vec = aligned(a, 16);
+    if (vec) {
+        // Regions of 4 K steps of a band where they tile K, else 2 (K is a
+        // multiple of 64); a block per region, up to 8192 blocks that loop.
+        const int steps = k / kFBK;
+        const bool four = steps % 4 == 0;
+        const long long regions = mchip_packed_a16_elements(m, k) / (kFBM * kFBK) / (four ? 4 : 2);
+        const dim3 rgrid(static_cast<unsigned>(std::max<long long>(1, std::min<long long>(regions, 8192))));
+        const f32x4* in = reinterpret_cast<const f32x4*>(a);
+        if (dtype == MCHIP_DTYPE_BF16 && four) {
+            hipLaunchKernelGGL((convert_pack_a_lds<true, 4>), rgrid, dim3(256), 0, s, in, out, m, k, regions);
+        } else if (dtype == MCHIP_DTYPE_BF16) {
+            hipLaunchKernelGGL((convert_pack_a_lds<true, 2>), rgrid, dim3(256), 0, s, in, out, m, k, regions);
+        } else if (four) {
+            hipLaunchKernelGGL((convert_pack_a_lds<false, 4>), rgrid, dim3(256), 0, s, in, out, m, k, regions);
+        } else {
+            hipLaunchKernelGGL((convert_pack_a_lds<false, 2>), rgrid, dim3(256), 0, s, in, out, m, k, regions);
+        }
+    } else if (dtype == MCHIP_DTYPE_BF16) {
+        hipLaunchKernelGGL((convert_pack_a_kernel<true>), grid, dim3(256), 0, s, a, out, m, k, chunks);
+    } else {
+        hipLaunchKernelGGL((convert_pack_a_kernel<false>), grid, dim3(256), 0, s, a, out, m, k, chunks);
+    }
+    return hipGetLastError();
+}
+
+extern "C" int mchip_launch_matmul_lowp_packed(int kernel, int dtype, const void* a_packed, const void* b, float* c,
+                                               int m, int n, int k, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (m < 1 || n < 1 || k < 1) return hipErrorInvalidValue;
+    if (kernel == kTensorCoreTf32) return hipErrorNotSupported;
+    if (!fast_eligible(a_packed, b, c, m, n, k, 1)) return hipErrorInvalidValue;
+    if (kernel == kTensorCoreBf16 && dtype == MCHIP_DTYPE_BF16) return launch_fast<true, true>(a_packed, b, c, m, n, k, s);
+    if (kernel == kTensorCoreF16 && dtype == MCHIP_DTYPE_F16) return launch_fast<false, true>(a_packed, b, c, m, n, k, s);
     return hipErrorInvalidValue;
 }
 

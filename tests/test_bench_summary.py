@@ -76,3 +76,15 @@ def test_single_workload_records_fit(workload):
     keep = {"gelu": ["gelu_4096x4096", "gelu_fusion_4096x4096"], "gemm_bf16": ["gemm_bf16_fp16"]}[workload]
     full["configs"] = {k: v for k, v in full["configs"].items() if k in keep}
     check_line(full)
+
+
+def test_bf16_rows_keep_each_a_layout_apart():
+    # The bf16/fp16 GEMM rows come in two A layouts (row-major, packed); the
+    # summary keys them apart, and both still fit.
+    full = recorded()
+    rows = full["configs"]["gemm_bf16_fp16"]
+    full["configs"]["gemm_bf16_fp16"] = [dict(e, a_layout=layout) for e in rows for layout in ("row-major", "packed")]
+    line = check_line(full)
+    keys = list(line["configs"]["gemm_bf16_fp16"]["rows"])
+    assert len(keys) == 2 * len(rows)
+    assert "bf16 8192x8192x8192" in keys and "bf16 8192x8192x8192 A packed" in keys

@@ -168,7 +168,7 @@ def test_generated_kernels_compile_for_gfx950_without_a_gpu(mc, text, shapes, ou
                                        ("narrow32", "mc_gemm_f32_narrow<McNarrow32>"),
                                        ("narrow16x64", "mc_gemm_f32_narrow<McNarrow16x64>"),
                                        ("narrow16x32", "mc_gemm_f32_narrow<McNarrow16x32>"),
-                                       ("bf16", "mc_gemm16_fast<true>"), ("f16", "mc_gemm16_fast<false>")])
+                                       ("bf16", "mc_gemm16_fast<true, true>"), ("f16", "mc_gemm16_fast<false, true>")])
 def test_every_gemm_body_with_an_epilogue_compiles_for_gfx950(mc, body, call):
     # bias + tanh on the product, as a fused group reads it: each GEMM body the
     # executable can pick, compiled by hipRTC with no device.

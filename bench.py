@@ -1113,7 +1113,7 @@ def main() -> int:
         if not args.quick:
             line.setdefault("configs", {})["copy_ceiling_128MiB"] = bench_copy_ceiling(mc, args.steps, args.warmup)
     elif args.workload in ("gelu", "batchnorm"):
-        k = next(iter(cfgs.values()))
+        k = cfgs["gelu_4096x4096" if args.workload == "gelu" else "batchnorm_relu_200704x256"]
         line.update({"value": k["gbs"], "unit": "GB/s", "ms_per_step": k["ms_per_step"], "dtype": "f32",
                      "steps": k["timed_steps"], "config": {"workload": k["config"], **k["dims"]},
                      "roofline": {"bound": "hbm", "kernel": k["kernel"]["launch"], "achieved": k["gbs"],

@@ -520,6 +520,9 @@ ElementwiseKernel generate_elementwise_kernel(const FusedProgram& program, const
         } else {
             os << indent << "\t" << store_stmt("p", call("")) << "\n";
         }
+        // Each item's store before the next item's arithmetic, so the
+        // stores go out spread over the step instead of bunched at its end.
+        os << indent << "\t__builtin_amdgcn_sched_barrier(0);\n";
         os << indent << "}\n";
     };
 

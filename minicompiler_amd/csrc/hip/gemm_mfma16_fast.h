@@ -90,10 +90,6 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 // On an MI355X the 8192^3 bf16 product took 787-795 us so against 840-845 us
 // with row-major A (timing copies, one process); the same layout for B
 // gained nothing (B's fetch already reads 512 bytes per k row).
-__device__ __forceinline__ long long mc_packed_a16_index(int row, int kk, int k) {
-    return static_cast<long long>(row >> 8) * 256 * k + static_cast<long long>(kk >> 5) * 8192 +
-           ((row & 255) >> 4) * 512 + ((kk & 31) >> 3) * 128 + (row & 15) * 8 + (kk & 7);
-}
 
 __device__ __forceinline__ int mc_min16(int a, int b) { return a < b ? a : b; }
 #define MC_LDS __attribute__((address_space(3)))

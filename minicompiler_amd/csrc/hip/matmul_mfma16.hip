@@ -249,7 +249,7 @@ int launch_fast(const void* a, const void* b, float* c, int m, int n, int k, hip
 
 // ------------------------------------------------------------ packed A
 //
-// One lane per 16-byte chunk of the packed layout (mc_packed_a16_index): 8
+// One lane per 16-byte chunk of the packed layout (gemm_mfma16_fast.h): 8
 // consecutive k of one row. Consecutive lanes take consecutive chunks, so a
 // wave writes 1 KiB of consecutive memory and reads 16 rows x 4 chunks
 // (64 bytes of 16-bit A, 128 of fp32 A, per row). Rows past M are zeros.

@@ -6,10 +6,11 @@ multiple of 32 and N of 4; vectorized always runs the two-stage body
 v_mfma_f32_32x32x2_f32 sequence, so the outputs must be identical bit for
 bit, and within the reference's dot-product bound
 (tests/test_cuda_backend.cpp:119-162). The shapes reach the ring
-configurations on a 256-CU MI355X (256x256 tiles with direct fetches;
-128x128 tiles with the fetch staged through registers, two blocks or one
-block per CU; 32x128 tiles for M <= 32), blocks that take several tiles,
-ragged edges and a grid that is not a multiple of 8."""
+configurations the planner picks on a 256-CU MI355X (128x128 tiles with the
+fetch staged through registers, in two 4-wave blocks or one 8-wave block per
+CU; 32x128 tiles for M <= 32), blocks that take several tiles, odd and even
+K-step counts, ragged edges and a grid that is not a multiple of 8; the fused
+test also forces the 256x256 tiles."""
 
 import numpy as np
 import pytest
@@ -20,13 +21,15 @@ pytestmark = pytest.mark.gpu
 
 GUARD = 4096  # floats after C, prefilled with NaN; must stay untouched
 
-# (m, k, n) and the configuration the plan picks on 256 CUs: 256x256 tiles,
-# ragged M and N (256 tiles); 256x256 tiles, two per block (512 tiles);
-# two 128x128 blocks per CU, ragged (512 tiles); the same with some CUs
-# holding one block (304 tiles); one 128x128 block per CU with a grid of 9
-# (not a multiple of 8) and with 256 tiles (the class of the MLP's second
-# GEMM); one row, one K step; M <= 32 (32x128 tiles, 6 stages), N ragged and
-# a grid of 33, and a single tile.
+# (m, k, n) and the configuration the plan picks on 256 CUs: 128x128 tiles in
+# two blocks per CU, ragged M and N, two tiles per block (1024 tiles); one K
+# step per tile and four tiles per block (2048 tiles: every other tile starts
+# the staged loop on an odd step); ragged, one tile per block (512 tiles);
+# three K steps (a pair of steps, then one) with some CUs holding one block
+# (304 tiles); one 8-wave block per CU with a grid of 9 (not a multiple of 8)
+# and with 256 tiles (the class of the MLP's second GEMM); one row, one K
+# step; M <= 32 (32x128 tiles, 6 stages), N ragged and a grid of 33; two
+# tiles. (256x256 tiles run only when forced: the fused test below.)
 SHAPES = [(4000, 64, 4000), (4096, 32, 8192), (4000, 64, 2000), (2048, 96, 2432), (300, 96, 260), (8192, 256, 512),
           (1, 32, 4), (16, 1024, 4100), (32, 64, 256)]
 

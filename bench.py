@@ -649,8 +649,9 @@ def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
     rounded once, at compile time), then runs the GEMM with bias+GELU fused
     into its store. `tflops` counts the GEMM's 2MNK FLOPs over the measured
     step (rounding of x included). The rounding of x alone (the same
-    conversion on a copy of x, timed the same way) is reported beside it as
-    `round_x_ms`, a separate measurement; nothing is subtracted."""
+    conversion into packed A, `mc_convert_pack_a_f32`, on a copy of x, timed
+    the same way) is reported beside it as `round_x_ms`, a separate
+    measurement; nothing is subtracted."""
     out = []
     for m, n, k in shapes:
         x = mc.uniform(m * k, 1, -1.0, 1.0)
@@ -663,9 +664,9 @@ def bench_lowp_epilogue(mc, shapes, steps: int, warmup: int) -> list[dict]:
             (j,) = [i for i, nm in enumerate(names) if nm.startswith("matmul")]
             launch_ms = t["launch_ms"][j]
             del c, bufs
-            xs = operand_sets(mc, [4 * m * k, 2 * m * k],
-                              lambda: (mc.DeviceBuffer.from_array(x), mc.DeviceBuffer(2 * m * k)))
-            rounds = [lambda st, a=a, h=h: mc.convert_f32(dtype, a.ptr, h.ptr, m * k, st) for a, h in xs]
+            pb = mc.packed_a16_bytes(m, k)
+            xs = operand_sets(mc, [4 * m * k, pb], lambda: (mc.DeviceBuffer.from_array(x), mc.DeviceBuffer(pb)))
+            rounds = [lambda st, a=a, h=h: mc.convert_pack_a_f32(dtype, a.ptr, h.ptr, m, k, st) for a, h in xs]
             round_ms = time_gemm(mc, rounds, steps, warmup)["graph"]["ms"]
             del xs, rounds
             tf = 2.0 * m * n * k / (t["ms_per_step"] * 1e-3) / 1e12

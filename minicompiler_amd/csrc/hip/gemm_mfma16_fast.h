@@ -206,32 +206,58 @@ __device__ __forceinline__ void step_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// The store of a wave's accumulators: acc[fi][fj] holds
-// C[row + 16 fi][col + 16 fj + v] (row, col include the lane's l % 16 and
-// 4 (l / 16)). kCheck: some rows or columns may be past the matrix edge.
-// Without it the store is straight-line code, so the compiler can issue the
-// epilogue's operand loads for many fragments before the first store.
+// Lane l takes the value of lane (l & ~15) | ((l + 8) & 15): a rotation by
+// 8 within each row of 16 lanes (DPP row_ror:8).
+__device__ __forceinline__ float mc_row_ror8(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+}
+
+// The store of a wave's accumulators, whose first row and column are (row,
+// col): lane l = 16 g + i of acc[fi][fj] holds
+// C[row + 16 fi + i][col + 16 fj + 4 g + v], v = 0..3, so a store straight
+// from one fragment writes 64 bytes in each of 16 rows, half of every
+// 128-byte line. Two neighbouring fragments (16 fj = 32 p and 32 p + 16)
+// cover 32 columns, whole lines: lanes with i >= 8 of the first swap with
+// lanes with i < 8 of the second (a rotation by 8 within each 16-lane row and
+// a select), after which one register holds rows 0-7 and the other rows
+// 8-15 of the pair, lane l at row 8 h + l % 8 and 16-byte chunk
+// l / 16 + 4 ((l / 8) % 2). Each store instruction then writes 8 whole lines.
+// kCheck: some rows or columns may be past the matrix edge.
 // Non-temporal: every CU stores its tile at the same moment, with its matrix
-// units idle until the next tile starts; at 8192^3 the kernel took 811 us
-// with plain stores, 777 us with these and 727 us with no store at all (a
-// timing-only variant), on one MI355X in one process.
+// units idle until the next tile starts. On one MI355X in one process, at
+// 8192^3 with A packed: 782 us with half-line stores, 766 us with whole
+// lines; on 4096x14336x4096 393 and 374 us; 708 us at 8192^3 with no store at
+// all (a timing-only variant). Plain stores instead of non-temporal ones
+// were slower (811 against 777 us with half lines).
 template <int kRowFrags, bool kCheck, typename Epilogue>
 __device__ __forceinline__ void fast_store(const mc_f32x4_t (&acc)[kRowFrags][kFColFrags], float* __restrict__ c,
-                                           int row, int col, int m, int n, const Epilogue& epilogue) {
+                                           int row, int col, int m, int n, int lane, const Epilogue& epilogue) {
+    const bool hi = (lane & 8) != 0;
+    const int lr = lane & 7;
+    const int chunk = (lane >> 4) + (hi ? 4 : 0);
 #pragma unroll
     for (int fi = 0; fi < kRowFrags; ++fi) {
-        const int r = row + fi * 16;
-        if (kCheck && r >= m) continue;
-        float* crow = c + static_cast<long long>(r) * n;
 #pragma unroll
-        for (int fj = 0; fj < kFColFrags; ++fj) {
-            const int cc = col + fj * 16;
-            if (kCheck && cc >= n) continue;
-            const unsigned at = static_cast<unsigned>(static_cast<long long>(r) * n + cc);
-            mc_f32x4_t v = acc[fi][fj];
+        for (int p = 0; p < kFColFrags / 2; ++p) {
+            const mc_f32x4_t fa = acc[fi][2 * p], fb = acc[fi][2 * p + 1];
+            mc_f32x4_t t[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = epilogue(v[e], at + e);
-            __builtin_nontemporal_store(v, reinterpret_cast<mc_f32x4_t*>(crow + cc));
+            for (int e = 0; e < 4; ++e) {
+                const float ra = mc_row_ror8(fa[e]), rb = mc_row_ror8(fb[e]);
+                t[0][e] = hi ? rb : fa[e];
+                t[1][e] = hi ? fb[e] : ra;
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int r = row + fi * 16 + 8 * h + lr;
+                const int cc = col + 32 * p + 4 * chunk;
+                if (kCheck && (r >= m || cc >= n)) continue;
+                const unsigned at = static_cast<unsigned>(static_cast<long long>(r) * n + cc);
+                mc_f32x4_t v = t[h];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = epilogue(v[e], at + e);
+                __builtin_nontemporal_store(v, reinterpret_cast<mc_f32x4_t*>(c + static_cast<long long>(r) * n + cc));
+            }
         }
     }
 }
@@ -281,7 +307,7 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
     L.b_step = 2 * kFBK * n;
     // Wave (wm, wn) of the 2x4 grid owns rows kRows / 2 wm .., columns 64 wn ...
     const int wr = (wave >> 2) * (kRows / 2), wc = (wave & 3) * 64;
-    const int li = lane & 15, g = lane >> 4;
+    const int g = lane >> 4;
 #pragma unroll
     for (int f = 0; f < Sh::kRowFrags; ++f) L.a_off[f] = (wr + f * 16) * 64 + lane * 16;
     // Transposed B reads: lane (g, e = (l % 16) / 4, cc = l % 4) points at
@@ -346,9 +372,9 @@ __device__ __forceinline__ void fast_tile(MC_LDS unsigned char* lds, const unsig
     __builtin_amdgcn_s_waitcnt(0);
 
     if (row0 + kRows <= m && col0 + kFBN <= n)
-        fast_store<Sh::kRowFrags, false>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+        fast_store<Sh::kRowFrags, false>(acc, c, row0 + wr, col0 + wc, m, n, lane, epilogue);
     else
-        fast_store<Sh::kRowFrags, true>(acc, c, row0 + wr + li, col0 + wc + 4 * g, m, n, epilogue);
+        fast_store<Sh::kRowFrags, true>(acc, c, row0 + wr, col0 + wc, m, n, lane, epilogue);
 }
 
 // C = A B with the epilogue mapping each accumulated value v of element

@@ -35,9 +35,10 @@ struct McGemm16Store {
 // K is walked in steps of 32 through a ring of four 32 KiB LDS stages, with
 // the two waves of each SIMD in ping-pong: waves 0-3 and waves 4-7 run the
 // same sequence one phase apart, alternating a memory phase (issue the
-// global -> LDS fetch of step t+3, read step t's operands from LDS into
-// registers) and a compute phase (step t's 32 MFMAs), so each SIMD's matrix
-// unit is fed by one wave while the other loads. Phases are separated by a
+// global -> LDS fetch of A for step t+3, read step t's operands from LDS into
+// registers) and a compute phase (step t's 32 MFMAs, with the fetch of B for
+// step t+3 issued after the first 16), so each SIMD's matrix unit is fed by
+// one wave while the other loads. Phases are separated by a
 // plain s_barrier of all 8 waves (no memory fence: a fence would also wait
 // for the fetches still in flight); a memory phase ends with a wait for this
 // wave's fetch of step t+1 and for its LDS reads.

@@ -15,9 +15,10 @@ pytestmark = pytest.mark.gpu
 
 FORMATS = [("tensor_core_bf16", 1, 2.0 ** -8, False), ("tensor_core_f16", 2, 2.0 ** -11, True)]
 # (m, k, n): tile-aligned, ragged M, ragged N (multiple of 8), tiny, several K tiles, a non-multiple-of-8 N and a
-# K that is not a multiple of 64 (general kernel).
+# K that is not a multiple of 64 (general kernel). The fast kernel stores C as 8-row by 32-column pieces: the
+# ragged shapes put the matrix edge at every offset within one (M % 16 = 12, 15, 8, 1; N % 32 = 8, 24, 16).
 SHAPES = [(256, 64, 256), (300, 128, 264), (1, 64, 8), (513, 192, 1000), (512, 1024, 768), (96, 256, 4100),
-          (200, 100, 136)]
+          (200, 100, 136), (271, 128, 280), (264, 64, 272)]
 GUARD = 4096  # floats after C, prefilled with NaN; must stay untouched
 
 

@@ -80,8 +80,10 @@ def test_convert_pack_rounds_as_convert_f32(device, mc, oracle, dtype, m, k):
 
 # (m, n, k): one tile; ragged M with every tile run as two 128-row halves (the
 # second half of the last band past M); 272 tiles with the last 16 as halves
-# and a ragged last band; ragged N; several rounds.
-SHAPES = [(256, 256, 64), (300, 520, 256), (4300, 4096, 64), (1000, 1032, 512), (2048, 2048, 1024)]
+# and a ragged last band; ragged N; several rounds; the matrix edge inside C's 8-row by 32-column store pieces
+# (M % 16 = 15 and 7, N % 32 = 24 and 16).
+SHAPES = [(256, 256, 64), (300, 520, 256), (4300, 4096, 64), (1000, 1032, 512), (2048, 2048, 1024), (271, 280, 128),
+          (263, 272, 192)]
 
 
 @pytest.mark.parametrize("kernel,dtype", [("tensor_core_bf16", 1), ("tensor_core_f16", 2)])

@@ -800,6 +800,16 @@ def cpu_baseline(batch_rows: int, seconds: float) -> dict:
     return e
 
 
+# The `config.workload` names of the bench line; profiles/traffic.json keys
+# its entries "<workload> | <launch>" by them.
+BF16_WORKLOAD = ("bf16 gemm 8192^3, bf16 inputs in HBM, A packed (mc_pack_a16's layout; the row-major row is in "
+                 "configs) (BASELINE config 5)")
+
+
+def mlp_workload(batch: int) -> str:
+    return f"mlp_gelu B={batch} D=512 H=2048 fp32 (BASELINE config 2)"
+
+
 def measured_traffic(workload: str, launch: str):
     """HBM bytes per launch of `launch` in `workload`, from the rocprofv3
     FETCH_SIZE and WRITE_SIZE runs summarised in profiles/traffic.json (each
@@ -1090,7 +1100,7 @@ def main() -> int:
         dom = max(ks, key=lambda e: e["ms"])
         line.update({"value": r["value"], "unit": "TFLOP/s", "ms_per_step": r["timing"]["ms_per_step"],
                      "dtype": "f32",
-                     "config": {"workload": f"mlp_gelu B={args.batch} D=512 H=2048 fp32 (BASELINE config 2)",
+                     "config": {"workload": mlp_workload(args.batch),
                                 "global_batch": args.batch, "matmul": ",".join(r["compiled"].matmul_kernels),
                                 "buffer_sets": r["buffer_sets"], "order": r["timing"]["order"]},
                      "host_us_per_step": r["timing"]["host_us_per_step"]})
@@ -1133,8 +1143,7 @@ def main() -> int:
         (top,) = [e for e in cfgs["gemm_bf16_fp16"] if e["kernel"] == "tensor_core_bf16" and e["m"] == 8192
                   and e["a_layout"] == "packed"]
         line.update({"value": top["tflops"], "unit": "TFLOP/s", "ms_per_step": top["ms"], "dtype": "bf16",
-                     "config": {"workload": "bf16 gemm 8192^3, bf16 inputs in HBM, A packed (mc_pack_a16's "
-                                            "layout; the row-major row is in configs) (BASELINE config 5)"},
+                     "config": {"workload": BF16_WORKLOAD},
                      "roofline": {"bound": "mfma", "kernel": top["kernel"], "achieved": top["tflops"],
                                   "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": top["frac"], "traffic": None}})
         if "cpu_baseline" in top:

@@ -88,3 +88,16 @@ def test_bf16_rows_keep_each_a_layout_apart():
     keys = list(line["configs"]["gemm_bf16_fp16"]["rows"])
     assert len(keys) == 2 * len(rows)
     assert "bf16 8192x8192x8192" in keys and "bf16 8192x8192x8192 A packed" in keys
+
+
+def test_the_counted_kernels_match_the_bench_lines_workload_names():
+    # roofline.traffic is looked up by "<config.workload> | <launch>": each
+    # workload whose dominant kernel was counted must keep the name the bench
+    # line gives it, or its traffic would silently read null.
+    kernels = json.loads((Path(bench.__file__).parent / "profiles" / "traffic.json").read_text())["kernels"]
+    workloads = {key.split(" | ")[0] for key in kernels}
+    assert bench.mlp_workload(8192) in workloads
+    assert bench.BF16_WORKLOAD in workloads
+    # At least the algorithmic bytes: A and B in bf16 (2 x 128 MiB) read, C in fp32 (256 MiB) written.
+    assert bench.measured_traffic(bench.BF16_WORKLOAD, "tensor_core_bf16") >= 2 ** 29
+    assert bench.measured_traffic(bench.BF16_WORKLOAD, "no such kernel") is None
